@@ -1,0 +1,101 @@
+/*
+ * w4a16.h -- C ABI of the MI355X (gfx950) INT4-weight / bf16-activation linear.
+ *
+ * Plain pointers and sizes only.  Every device pointer is borrowed: the caller
+ * owns and allocates all buffers (inputs, output and workspace), so a call never
+ * allocates and can be captured into a HIP graph.  Work is enqueued on `stream`
+ * (a hipStream_t passed as void*; NULL means the default stream).  No exception
+ * crosses this boundary: every entry point returns a W4A16_* status code.
+ *
+ * Data layout (the reference format, engine/kernels/quant.py:81-119):
+ *   x       bf16  [M, K]     row stride ldx elements, unit column stride
+ *   packed  int8  [K/2, N]   row stride ldp bytes; byte (i, n) holds q[2i, n] in
+ *                            bits 7..4 and q[2i+1, n] in bits 3..0, both 4-bit
+ *                            two's complement
+ *   scale   fp32  [K/g, N]   row stride lds elements, g = group_size
+ *   y       bf16  [M, N]     row stride ldy elements
+ */
+#ifndef W4A16_H_
+#define W4A16_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W4A16_ABI_VERSION 1
+
+/* Status codes. */
+#define W4A16_OK 0
+#define W4A16_ERR_NULL 1        /* a required pointer is NULL */
+#define W4A16_ERR_SHAPE 2       /* negative size, or a leading dimension smaller than the row */
+#define W4A16_ERR_K_GROUP 3     /* K not a multiple of group_size, or odd */
+#define W4A16_ERR_GROUP_SIZE 4  /* group_size unsupported (linear: must be 128) */
+#define W4A16_ERR_WORKSPACE 5   /* workspace NULL or smaller than w4a16_workspace_size() */
+#define W4A16_ERR_LAUNCH 6      /* a HIP launch reported an error */
+#define W4A16_ERR_DTYPE 7       /* unknown dtype code */
+#define W4A16_ERR_TOO_LARGE 8   /* N exceeds the split-K counter table (4,194,304 columns) */
+
+/* dtype codes for w4a16_dequant. */
+#define W4A16_DTYPE_F32 0
+#define W4A16_DTYPE_BF16 1
+
+/* Version of this ABI (W4A16_ABI_VERSION of the build). */
+int w4a16_abi_version(void);
+
+/* Static description of a status code. */
+const char* w4a16_error_string(int code);
+
+/*
+ * Bytes of device workspace w4a16_linear needs for an (M, N, K) call; 0 means
+ * the call needs none.  The first 64 KiB of a workspace are split-K arrival
+ * counters: they must be zero before the first call that uses the buffer and
+ * are left at zero by every completed call, so a buffer is zeroed once when it
+ * is allocated.  Calls that share a workspace must be ordered (same stream).
+ * Replaces no reference entry point: the reference kernel needs no workspace
+ * (engine/kernels/quant.py:270-280 allocates only the output).
+ */
+int w4a16_workspace_size(int M, int N, int K, int group_size, size_t* bytes);
+
+/*
+ * y[M, N] = x[M, K] @ dequant(packed, scale)[K, N], bf16 output, fp32
+ * accumulation, per-group partial products scaled in fp32.
+ *
+ * Replaces the device branch of int4_matmul (engine/kernels/quant.py:267-281),
+ * i.e. the launch of _int4_matmul_kernel (engine/kernels/quant.py:159-240), and
+ * with it the whole of _Int4Weight.fused_linear (engine/quantize.py:64-73)
+ * once the caller has flattened x to [M, K].
+ *
+ * group_size must be 128 (the reference asserts the same,
+ * engine/kernels/quant.py:267).  K must be a multiple of 128.  M == 0 or
+ * N == 0 is a no-op; K == 0 writes zeros.  M <= 32 runs the bandwidth-bound
+ * skinny kernel, M > 32 the MFMA GEMM.
+ */
+int w4a16_linear(const void* x, int64_t ldx,
+                 const int8_t* packed, int64_t ldp,
+                 const float* scale, int64_t lds,
+                 void* y, int64_t ldy,
+                 int M, int N, int K, int group_size,
+                 void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/*
+ * out[K, N] = q[K, N] * scale[k / group_size, n]  in fp32 (out_dtype
+ * W4A16_DTYPE_F32), or with scale and product both rounded to bf16
+ * (W4A16_DTYPE_BF16), i.e. dequantize_weight_int4(packed, scale.to(dtype))
+ * of engine/kernels/quant.py:122-156 for dtype float32 / bfloat16.  Any
+ * group_size > 0 dividing K.  Row stride of out: ldo elements.
+ */
+int w4a16_dequant(const int8_t* packed, int64_t ldp,
+                  const float* scale, int64_t lds,
+                  void* out, int64_t ldo, int out_dtype,
+                  int K, int N, int group_size,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A16_H_ */

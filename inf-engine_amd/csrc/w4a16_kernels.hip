@@ -1,0 +1,787 @@
+// W4A16 fused linear for MI355X (gfx950): y[M,N] = x[M,K] (bf16) @ W[K,N],
+// W stored as packed signed INT4 with one fp32 scale per 128-row K group.
+//
+// Weight format (fixed by the reference, engine/kernels/quant.py:115-118,141-146):
+//   packed[k/2, n] int8: bits 7..4 = q[2i, n] (even K row), bits 3..0 = q[2i+1, n]
+//   (odd K row), both 4-bit two's complement in [-8, 7];
+//   scale[k/128, n] fp32;  W[k, n] = q[k, n] * scale[k/128, n].
+// Contraction order (engine/kernels/quant.py:221-234): per 128-row group the dot
+// product of bf16 activations with the integer weights is formed in fp32, then
+// multiplied by the fp32 scale and added to an fp32 accumulator; the result is
+// rounded once to bf16.
+//
+// Kernels in this file:
+//   skinny_kernel   M <= 32 (decode, batched decode, speculative verify).  HBM bound.
+//   rowsum_kernel   per-(group,row) activation sums used by gemm_kernel.
+//   gemm_kernel     M > 32 (prefill).  MFMA bound.
+//   dequant_kernel  packed -> dense weights (bit-exactness probe of the unpack).
+//
+// Nibble -> bf16 conversion used by both matrix kernels.  Flipping bit 3 of a
+// two's complement nibble q gives u = q + 8 in [0, 15].  The bf16 bit pattern
+// 0x4300 | u is exactly 128 + u, so one byte permute plus one and-or turns a
+// packed byte into a pair of bf16 values (128 + u_even, 128 + u_odd).  The MFMA
+// therefore produces sum_k x[k] * (q[k] + 136); the 136 * sum_k x[k] offset is
+// removed per (row, group) before the scale is applied, which keeps the
+// per-group partial exact up to fp32 accumulation rounding.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/w4a16.h"
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kGroup = 128;                 // K rows per scale group
+constexpr int kPackedRowsPerGroup = kGroup / 2;
+constexpr uint32_t kBf16Base = 0x43004300u; // bf16 128.0 in both halves
+constexpr uint32_t kBf16Neg136 = 0xC308C308u;
+constexpr float kOffset = 136.0f;           // 128 (bf16 base) + 8 (nibble bias)
+constexpr int kCounterBytes = 65536;        // split-K arrival counters at the head of the workspace
+constexpr int kMaxStrips = kCounterBytes / 4;
+
+struct LinearArgs {
+  const uint16_t* x;   // bf16 activations [M, K], row stride ldx (elements)
+  int64_t ldx;
+  const uint8_t* packed;  // [K/2, N], row stride ldp (bytes)
+  int64_t ldp;
+  const float* scale;  // [K/128, N], row stride lds (elements)
+  int64_t lds;
+  uint16_t* y;         // bf16 output [M, N], row stride ldy (elements)
+  int64_t ldy;
+  int M, N, K;
+  float* part;         // split-K partials [nsplit][M][N] (skinny) / row sums [K/128][M] (gemm)
+  uint32_t* counters;  // one arrival counter per column strip, zero between calls
+  int gps;             // groups per split (skinny)
+  int nsplit;          // number of K splits (skinny)
+  int vec;             // bit 0: packed/scale rows 16B aligned; bit 1: x rows 16B aligned;
+                       // bit 2: y rows 8B aligned
+  int mtiles, ntiles;  // gemm tile grid
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float((uint32_t)h << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16; NaN becomes the canonical quiet NaN 0x7FC0,
+// the same rule torch uses for float -> bfloat16.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// A 32-bit word of packed bytes (4 columns) prepared for pair extraction.
+struct Prep {
+  uint32_t p;  // nibble sign bits flipped: every nibble now holds u = q + 8
+  uint32_t q;  // p >> 4: the high nibble of byte c sits in the low nibble of byte c
+};
+
+__device__ __forceinline__ Prep prep(uint32_t raw) {
+  Prep w;
+  w.p = raw ^ 0x88888888u;
+  w.q = w.p >> 4;
+  return w;
+}
+
+// bf16 pair for column c (0..3) of a prepared word: low half 128 + u(even row),
+// high half 128 + u(odd row).
+template <int C>
+__device__ __forceinline__ uint32_t pair_of(Prep w) {
+  // v_perm_b32 byte pool: bytes 0-3 come from the second operand, 4-7 from the first.
+  const uint32_t y = __builtin_amdgcn_perm(w.p, w.q, (uint32_t)C | ((uint32_t)(4 + C) << 16));
+  return (y & 0x000F000Fu) | kBf16Base;
+}
+
+__device__ __forceinline__ uint32_t pair_dyn(Prep w, int c) {
+  switch (c) {
+    case 0: return pair_of<0>(w);
+    case 1: return pair_of<1>(w);
+    case 2: return pair_of<2>(w);
+    default: return pair_of<3>(w);
+  }
+}
+
+// Load `bytes` (4, 8 or 16) consecutive packed bytes starting at column `col`
+// of one packed row.  Columns at or beyond N read as 0 (q = 0).
+template <int BYTES>
+__device__ __forceinline__ void load_packed(const uint8_t* row, int col, int N, bool vec,
+                                            uint32_t (&out)[BYTES / 4]) {
+  if (vec && col + BYTES <= N) {
+    if constexpr (BYTES == 16) {
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(row + col);
+      out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
+    } else if constexpr (BYTES == 8) {
+      u32x2_t v = *reinterpret_cast<const u32x2_t*>(row + col);
+      out[0] = v[0]; out[1] = v[1];
+    } else {
+      out[0] = *reinterpret_cast<const uint32_t*>(row + col);
+    }
+  } else {
+#pragma unroll
+    for (int w = 0; w < BYTES / 4; ++w) {
+      uint32_t acc = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int c = col + 4 * w + b;
+        const uint32_t v = (c < N) ? (uint32_t)row[c] : 0u;
+        acc |= v << (8 * b);
+      }
+      out[w] = acc;
+    }
+  }
+}
+
+// Load `CNT` consecutive fp32 scales from column `col`; columns >= N read 0.
+template <int CNT>
+__device__ __forceinline__ void load_scales(const float* row, int col, int N, bool vec, float (&s)[CNT]) {
+  if (vec && col + CNT <= N) {
+#pragma unroll
+    for (int i = 0; i < CNT; i += 4) {
+      f32x4_t v = *reinterpret_cast<const f32x4_t*>(row + col + i);
+      s[i] = v[0]; s[i + 1] = v[1]; s[i + 2] = v[2]; s[i + 3] = v[3];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < CNT; ++i) s[i] = (col + i < N) ? row[col + i] : 0.0f;
+  }
+}
+
+// 8 consecutive bf16 activations of one row (16 bytes).
+__device__ __forceinline__ bf16x8_t load_x8(const uint16_t* p, bool vec) {
+  if (vec) return *reinterpret_cast<const bf16x8_t*>(p);
+  u32x4_t v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = (uint32_t)p[2 * i] | ((uint32_t)p[2 * i + 1] << 16);
+  return as_bf16x8(v);
+}
+
+// ---------------------------------------------------------------------------
+// Skinny kernel (M <= 32).
+//
+// A wave owns 16*CPL output columns and a set of 128-row K groups.  Lane l
+// covers columns col0 = n0 + CPL*(l%16) .. +CPL and, inside each 32-row K step,
+// rows 8*(l/16) .. +8 (four packed rows).  Per group a lane issues 16 loads of
+// CPL bytes (4 steps x 4 packed rows); 16 lanes read CPL*16 contiguous bytes of
+// one packed row, so each wave load instruction covers four full row segments.
+// Column t of the lane maps to MFMA instance t with virtual column l%16, so the
+// lane's CPL output columns are contiguous.  MT M-subtiles of 16 rows reuse the
+// same unpacked weights.
+//
+// Per group g and M-subtile:  acc = -136*sum_k x  (4 MFMAs against a -136 matrix),
+// acc += x . (q + 136) over the 4 K steps, total += acc * scale[g, n].
+//
+// The 4 waves of a workgroup split the workgroup's groups round-robin and are
+// summed through LDS.  Workgroups along gridDim.y split K further; each writes
+// an fp32 partial and the last one to arrive for a column strip (arrival
+// counter) adds the partials in split order and writes bf16.  The counter is
+// reset to zero by that last workgroup, so the workspace needs zeroing once.
+// ---------------------------------------------------------------------------
+template <int MT, int CPL>
+__global__ __launch_bounds__(256) void skinny_kernel(LinearArgs a) {
+  constexpr int WPR = CPL / 4;       // 32-bit words per packed row per lane
+  constexpr int WCOLS = 16 * CPL;    // columns per wave / workgroup
+  extern __shared__ float red[];     // [4 waves][R rows][WCOLS]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lc = lane & 15;
+  const int lk = lane >> 4;
+  const int strip = blockIdx.x;
+  const int n0 = strip * WCOLS;
+  const int col0 = n0 + lc * CPL;
+  const int G = a.K / kGroup;
+  const int g_begin = blockIdx.y * a.gps;
+  const int g_end = min(G, g_begin + a.gps);
+  const bool vec_w = (a.vec & 1) != 0;
+  const bool vec_x = (a.vec & 2) != 0;
+  const int M = a.M;
+  const int N = a.N;
+
+  f32x4_t total[MT][CPL];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) total[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const bf16x8_t neg136 = as_bf16x8(u32x4_t{kBf16Neg136, kBf16Neg136, kBf16Neg136, kBf16Neg136});
+
+  for (int g = g_begin + wave; g < g_end; g += 4) {
+    // Packed weights of this group: 4 K steps x 4 packed rows x CPL bytes.
+    uint32_t raw[4][4][WPR];
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
+        load_packed<CPL>(a.packed + pr * a.ldp, col0, N, vec_w, raw[st][r]);
+      }
+
+    // Activations: lane holds x[m][g*128 + 32*st + 8*lk .. +8] for m = 16*mt + lc.
+    bf16x8_t A[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = mt * 16 + lc;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        if (m < M) {
+          A[mt][st] = load_x8(a.x + (int64_t)m * a.ldx + (int64_t)g * kGroup + st * 32 + lk * 8, vec_x);
+        } else {
+          A[mt][st] = as_bf16x8(u32x4_t{0u, 0u, 0u, 0u});
+        }
+      }
+    }
+
+    float s[CPL];
+    load_scales<CPL>(a.scale + (int64_t)g * a.lds, col0, N, vec_w, s);
+
+    // Offset correction -136 * sum_{k in group} x[m, k], in MFMA output layout.
+    f32x4_t cinit[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) c = mfma16(A[mt][st], neg136, c);
+      cinit[mt] = c;
+    }
+
+#pragma unroll
+    for (int wi = 0; wi < WPR; ++wi) {
+      Prep pw[4][4];
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pw[st][r] = prep(raw[st][r][wi]);
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) {
+        const int t = wi * 4 + c4;
+        bf16x8_t B[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          B[st] = as_bf16x8(u32x4_t{pair_dyn(pw[st][0], c4), pair_dyn(pw[st][1], c4),
+                                    pair_dyn(pw[st][2], c4), pair_dyn(pw[st][3], c4)});
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          f32x4_t acc = cinit[mt];
+#pragma unroll
+          for (int st = 0; st < 4; ++st) acc = mfma16(A[mt][st], B[st], acc);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) total[mt][t][r] = __builtin_fmaf(acc[r], s[t], total[mt][t][r]);
+        }
+      }
+    }
+  }
+
+  // ---- reduce the 4 waves through LDS (rows < M only) ----
+  const int R = min(M, 16 * MT);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = mt * 16 + lk * 4 + r;
+      if (m < R) {
+        float* dst = red + ((size_t)wave * R + m) * WCOLS + lc * CPL;
+#pragma unroll
+        for (int t = 0; t < CPL; t += 4)
+          *reinterpret_cast<f32x4_t*>(dst + t) =
+              f32x4_t{total[mt][t][r], total[mt][t + 1][r], total[mt][t + 2][r], total[mt][t + 3][r]};
+      }
+    }
+  __syncthreads();
+
+  const int elems = R * WCOLS;
+  if (a.nsplit == 1) {
+    for (int e = threadIdx.x; e < elems; e += 256) {
+      const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
+      if (n < N) {
+        float v = red[e];
+        v += red[(size_t)1 * elems + e];
+        v += red[(size_t)2 * elems + e];
+        v += red[(size_t)3 * elems + e];
+        a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(v);
+      }
+    }
+    return;
+  }
+
+  // ---- split-K: publish this split's partial, last arrival finishes the strip ----
+  float* part = a.part + (size_t)blockIdx.y * M * N;
+  for (int e = threadIdx.x; e < elems; e += 256) {
+    const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
+    if (n < N) {
+      float v = red[e];
+      v += red[(size_t)1 * elems + e];
+      v += red[(size_t)2 * elems + e];
+      v += red[(size_t)3 * elems + e];
+      part[(size_t)m * N + n] = v;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  __shared__ int is_last;
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(a.counters + strip, 1u, __ATOMIC_ACQ_REL,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (prev == (uint32_t)(a.nsplit - 1));
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  for (int e = threadIdx.x; e < elems; e += 256) {
+    const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
+    if (n < N) {
+      float v = 0.f;
+      for (int sp = 0; sp < a.nsplit; ++sp)
+        v += __builtin_nontemporal_load(a.part + ((size_t)sp * M + m) * N + n);
+      a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(v);
+    }
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.counters + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Row sums for the gemm offset correction: out[g*M + m] = 136 * sum_{k in g} x[m,k].
+// 16 lanes per (row, group); each lane sums 8 values, then a butterfly over the
+// 16 lanes (fixed order, deterministic).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rowsum_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M,
+                                                     int K, int vec_x, float* __restrict__ out) {
+  const int G = K / kGroup;
+  const int64_t item = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  const bool valid = item < (int64_t)M * G;
+  const int m = valid ? (int)(item / G) : 0;
+  const int g = valid ? (int)(item % G) : 0;
+  float s = 0.f;
+  if (valid) {
+    const bf16x8_t v = load_x8(x + (int64_t)m * ldx + (int64_t)g * kGroup + sub * 8, vec_x != 0);
+    const u32x4_t w = __builtin_bit_cast(u32x4_t, v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s += __uint_as_float(w[i] << 16);
+      s += __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) s += __shfl_xor(s, off, 16);
+  if (valid && sub == 0) out[(int64_t)g * M + m] = kOffset * s;
+}
+
+// ---------------------------------------------------------------------------
+// GEMM kernel (M > 32).
+//
+// Workgroup tile 128 rows x 256 columns, 4 waves side by side along N, each
+// wave 128 x 64.  Per 128-row K group the workgroup stages the activation tile
+// (128 x 128 bf16, 32 KB) in LDS in MFMA fragment order, double buffered, and
+// each wave keeps its own packed weights in registers (4 columns per lane, 16
+// loads of 4 bytes per group), unpacks them once into 16 bf16 B fragments and
+// applies them to the 8 M-subtiles:
+//   acc = -rowsum*136 ; acc += x . (q + 136) over 4 K steps ; total += acc * scale.
+// Tiles are handed out XCD-major: workgroup b runs on XCD b % 8, and each XCD
+// receives a contiguous range of tile ids, ordered in column bands of 4 row
+// tiles, so the rows of x and the weight columns an XCD touches stay in its L2.
+// ---------------------------------------------------------------------------
+constexpr int kGemmRows = 128;
+constexpr int kGemmCols = 256;
+constexpr int kGemmMT = 8;      // 16-row subtiles per wave
+constexpr int kGemmBand = 4;    // row tiles per column band
+
+__global__ __launch_bounds__(256) void gemm_kernel(LinearArgs a) {
+  __shared__ u32x4_t As[2][4 * kGemmMT * 64];  // [buf][step][subtile][lane] 16 B each
+  __shared__ __attribute__((aligned(16))) float Cs[2][kGemmRows];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lc = lane & 15;
+  const int lk = lane >> 4;
+  const int M = a.M, N = a.N;
+  const int G = a.K / kGroup;
+
+  // ---- tile assignment ----
+  const int tiles = a.mtiles * a.ntiles;
+  int tid_lin = blockIdx.x;
+  if ((gridDim.x & 7) == 0) {
+    const int per_xcd = gridDim.x >> 3;
+    tid_lin = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  }
+  if (tid_lin >= tiles) return;
+  const int band_size = kGemmBand * a.ntiles;
+  const int band = tid_lin / band_size;
+  const int first_m = band * kGemmBand;
+  const int band_rows = min(kGemmBand, a.mtiles - first_m);
+  const int in_band = tid_lin % band_size;
+  const int m_tile = first_m + in_band % band_rows;
+  const int n_tile = in_band / band_rows;
+
+  const int m0 = m_tile * kGemmRows;
+  const int col0 = n_tile * kGemmCols + wave * 64 + lc * 4;
+  const bool vec_w = (a.vec & 1) != 0;
+
+  // ---- staging helpers ----
+  // Wave w stages K step w: 8 subtiles x 64 lanes x 16 B.  Lane l of subtile i
+  // loads row m0 + 16*i + l%16, columns 8*(4*w + l/16) .. +8 of the group.
+  auto stage_a_load = [&](int g, u32x4_t (&buf)[kGemmMT]) {
+#pragma unroll
+    for (int i = 0; i < kGemmMT; ++i) {
+      int row = m0 + 16 * i + lc;
+      row = row < M ? row : M - 1;  // rows past M compute garbage that is never stored
+      const uint16_t* p = a.x + (int64_t)row * a.ldx + (int64_t)g * kGroup + (wave * 4 + lk) * 8;
+      buf[i] = *reinterpret_cast<const u32x4_t*>(p);
+    }
+  };
+  auto stage_a_store = [&](int b, const u32x4_t (&buf)[kGemmMT]) {
+#pragma unroll
+    for (int i = 0; i < kGemmMT; ++i) As[b][(wave * kGemmMT + i) * 64 + lane] = buf[i];
+  };
+  auto stage_c_load = [&](int g) -> float {
+    const int row = m0 + threadIdx.x;
+    return (threadIdx.x < kGemmRows && row < M) ? a.part[(int64_t)g * M + row] : 0.f;
+  };
+  auto load_b = [&](int g, uint32_t (&raw)[4][4]) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
+        uint32_t w[1];
+        load_packed<4>(a.packed + pr * a.ldp, col0, N, vec_w, w);
+        raw[st][r] = w[0];
+      }
+  };
+
+  f32x4_t total[kGemmMT][4];
+#pragma unroll
+  for (int i = 0; i < kGemmMT; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) total[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  uint32_t raw[4][4];
+  float s[4];
+  {
+    u32x4_t abuf[kGemmMT];
+    stage_a_load(0, abuf);
+    const float cv = stage_c_load(0);
+    load_b(0, raw);
+    load_scales<4>(a.scale, col0, N, vec_w, s);
+    stage_a_store(0, abuf);
+    if (threadIdx.x < kGemmRows) Cs[0][threadIdx.x] = cv;
+  }
+
+  for (int g = 0; g < G; ++g) {
+    const int b = g & 1;
+    __syncthreads();
+
+    // Prefetch the next group while this one computes.
+    const bool has_next = g + 1 < G;
+    u32x4_t abuf[kGemmMT];
+    uint32_t raw_n[4][4];
+    float s_n[4];
+    float cv_n = 0.f;
+    if (has_next) {
+      stage_a_load(g + 1, abuf);
+      cv_n = stage_c_load(g + 1);
+      load_b(g + 1, raw_n);
+      load_scales<4>(a.scale + (int64_t)(g + 1) * a.lds, col0, N, vec_w, s_n);
+    }
+
+    // Unpack this wave's weights for the whole group: B[step][column].
+    bf16x8_t B[4][4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      Prep p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = prep(raw[st][r]);
+      B[st][0] = as_bf16x8(u32x4_t{pair_of<0>(p[0]), pair_of<0>(p[1]), pair_of<0>(p[2]), pair_of<0>(p[3])});
+      B[st][1] = as_bf16x8(u32x4_t{pair_of<1>(p[0]), pair_of<1>(p[1]), pair_of<1>(p[2]), pair_of<1>(p[3])});
+      B[st][2] = as_bf16x8(u32x4_t{pair_of<2>(p[0]), pair_of<2>(p[1]), pair_of<2>(p[2]), pair_of<2>(p[3])});
+      B[st][3] = as_bf16x8(u32x4_t{pair_of<3>(p[0]), pair_of<3>(p[1]), pair_of<3>(p[2]), pair_of<3>(p[3])});
+    }
+
+#pragma unroll
+    for (int i = 0; i < kGemmMT; ++i) {
+      bf16x8_t A[4];
+#pragma unroll
+      for (int st = 0; st < 4; ++st) A[st] = __builtin_bit_cast(bf16x8_t, As[b][(st * kGemmMT + i) * 64 + lane]);
+      const f32x4_t c4 = *reinterpret_cast<const f32x4_t*>(&Cs[b][16 * i + 4 * lk]);
+      const f32x4_t cinit = -c4;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        f32x4_t acc = cinit;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) acc = mfma16(A[st], B[st][t], acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) total[i][t][r] = __builtin_fmaf(acc[r], s[t], total[i][t][r]);
+      }
+    }
+
+    if (has_next) {
+      stage_a_store(b ^ 1, abuf);
+      if (threadIdx.x < kGemmRows) Cs[b ^ 1][threadIdx.x] = cv_n;
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) raw[st][r] = raw_n[st][r];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) s[t] = s_n[t];
+    }
+  }
+
+  // ---- store: lane holds rows m0 + 16i + 4lk + r, columns col0 .. col0+3 ----
+  const bool vec_y = (a.vec & 4) != 0 && col0 + 4 <= N;
+#pragma unroll
+  for (int i = 0; i < kGemmMT; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 16 * i + 4 * lk + r;
+      if (m >= M) continue;
+      uint16_t* dst = a.y + (int64_t)m * a.ldy + col0;
+      const uint16_t h0 = f32_to_bf16(total[i][0][r]);
+      const uint16_t h1 = f32_to_bf16(total[i][1][r]);
+      const uint16_t h2 = f32_to_bf16(total[i][2][r]);
+      const uint16_t h3 = f32_to_bf16(total[i][3][r]);
+      if (vec_y) {
+        *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{(uint32_t)h0 | ((uint32_t)h1 << 16),
+                                                   (uint32_t)h2 | ((uint32_t)h3 << 16)};
+      } else {
+        if (col0 + 0 < N) dst[0] = h0;
+        if (col0 + 1 < N) dst[1] = h1;
+        if (col0 + 2 < N) dst[2] = h2;
+        if (col0 + 3 < N) dst[3] = h3;
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Dequantize: out[k, n] = q[k, n] * s[k/128, n] (engine/kernels/quant.py:122-156).
+// With a bf16 output the scale is first rounded to bf16, then the product is
+// rounded to bf16, which is what `dequantize_weight_int4(packed, scale.to(bf16))`
+// computes.  One thread per packed byte.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ packed, int64_t ldp,
+                                                      const float* __restrict__ scale, int64_t lds,
+                                                      void* __restrict__ out, int64_t ldo, int out_bf16,
+                                                      int K, int N, int group_size) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)(K / 2) * N;
+  if (idx >= total) return;
+  const int i = (int)(idx / N);
+  const int n = (int)(idx % N);
+  const int8_t byte = (int8_t)packed[(int64_t)i * ldp + n];
+  const int q_even = byte >> 4;                          // arithmetic shift: [-8, 7]
+  const int q_odd = (int)(int8_t)(uint8_t)(byte << 4) >> 4;
+  const int k = 2 * i;
+  float s = scale[(int64_t)(k / group_size) * lds + n];
+  if (out_bf16) {
+    s = bf16_to_f32(f32_to_bf16(s));
+    uint16_t* o = static_cast<uint16_t*>(out);
+    o[(int64_t)k * ldo + n] = f32_to_bf16((float)q_even * s);
+    o[(int64_t)(k + 1) * ldo + n] = f32_to_bf16((float)q_odd * s);
+  } else {
+    float* o = static_cast<float*>(out);
+    o[(int64_t)k * ldo + n] = (float)q_even * s;
+    o[(int64_t)(k + 1) * ldo + n] = (float)q_odd * s;
+  }
+}
+
+// y = 0 for an empty contraction (K == 0), as the reference produces.
+__global__ __launch_bounds__(256) void zero_kernel(uint16_t* __restrict__ y, int64_t ldy, int M, int N) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)M * N) return;
+  y[(idx / N) * ldy + idx % N] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side planning.
+// ---------------------------------------------------------------------------
+struct Plan {
+  int kind;    // 0 = skinny, 1 = gemm
+  int mt, cpl; // skinny variant
+  int strips, nsplit, gps;
+  size_t ws_bytes;
+};
+
+inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+Plan make_plan(int M, int N, int K) {
+  Plan p{};
+  const int G = K / kGroup;
+  if (M > 32) {
+    p.kind = 1;
+    p.ws_bytes = (size_t)kCounterBytes + (size_t)G * M * sizeof(float);
+    return p;
+  }
+  p.kind = 0;
+  p.mt = M <= 16 ? 1 : 2;
+  p.cpl = (p.mt == 1 && N >= 4096) ? 16 : 8;
+  p.strips = ceil_div(N, 16 * p.cpl);
+  // Enough workgroups to keep every CU streaming (~2 per CU), bounded so the
+  // fp32 partial traffic (write + read) stays within a quarter of the weight bytes.
+  const int want = ceil_div(512, p.strips);
+  const int by_traffic = (int)((int64_t)K / (64 * (int64_t)M));
+  int nsplit = want;
+  if (nsplit > by_traffic) nsplit = by_traffic;
+  const int max_split = ceil_div(G, 4);  // at least one group per wave
+  if (nsplit > max_split) nsplit = max_split;
+  if (nsplit < 1) nsplit = 1;
+  p.gps = G > 0 ? ceil_div(G, nsplit) : 0;
+  p.nsplit = G > 0 ? ceil_div(G, p.gps) : 1;
+  p.ws_bytes = p.nsplit > 1 ? (size_t)kCounterBytes + (size_t)p.nsplit * M * N * sizeof(float) : 0;
+  return p;
+}
+
+int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? W4A16_OK : W4A16_ERR_LAUNCH;
+}
+
+template <int MT, int CPL>
+int launch_skinny(const LinearArgs& a, const Plan& p, hipStream_t stream) {
+  const int R = a.M < 16 * MT ? a.M : 16 * MT;
+  const size_t shmem = (size_t)4 * R * 16 * CPL * sizeof(float);
+  hipLaunchKernelGGL((skinny_kernel<MT, CPL>), dim3(p.strips, p.nsplit), dim3(256), shmem, stream, a);
+  return launch_status();
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int w4a16_abi_version(void) { return W4A16_ABI_VERSION; }
+
+const char* w4a16_error_string(int code) {
+  switch (code) {
+    case W4A16_OK: return "ok";
+    case W4A16_ERR_NULL: return "null pointer argument";
+    case W4A16_ERR_SHAPE: return "invalid shape (negative size or leading dimension smaller than the row)";
+    case W4A16_ERR_K_GROUP: return "K must be a multiple of group_size (and even) for int4 packing";
+    case W4A16_ERR_GROUP_SIZE: return "fused INT4 kernel requires group_size=128";
+    case W4A16_ERR_WORKSPACE: return "workspace missing or smaller than w4a16_workspace_size()";
+    case W4A16_ERR_LAUNCH: return "HIP kernel launch failed";
+    case W4A16_ERR_DTYPE: return "unsupported dtype code";
+    case W4A16_ERR_TOO_LARGE: return "problem exceeds the supported size";
+    default: return "unknown w4a16 error";
+  }
+}
+
+int w4a16_workspace_size(int M, int N, int K, int group_size, size_t* bytes) {
+  if (!bytes) return W4A16_ERR_NULL;
+  *bytes = 0;
+  if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
+  if (group_size != kGroup) return W4A16_ERR_GROUP_SIZE;
+  if (K % kGroup != 0) return W4A16_ERR_K_GROUP;
+  if (M == 0 || N == 0) return W4A16_OK;
+  const Plan p = make_plan(M, N, K);
+  *bytes = p.ws_bytes;
+  return W4A16_OK;
+}
+
+int w4a16_linear(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, const float* scale,
+                 int64_t lds, void* y, int64_t ldy, int M, int N, int K, int group_size, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
+  if (group_size != kGroup) return W4A16_ERR_GROUP_SIZE;
+  if (K % kGroup != 0) return W4A16_ERR_K_GROUP;
+  if (M == 0 || N == 0) return W4A16_OK;
+  if (!y) return W4A16_ERR_NULL;
+  if (K > 0 && (!x || !packed || !scale)) return W4A16_ERR_NULL;
+  if (ldy < N || (K > 0 && (ldx < K || ldp < N || lds < N))) return W4A16_ERR_SHAPE;
+
+  const Plan p = make_plan(M, N, K);
+  if (p.ws_bytes > 0 && (!workspace || workspace_bytes < p.ws_bytes)) return W4A16_ERR_WORKSPACE;
+  if (p.kind == 0 && p.nsplit > 1 && p.strips > kMaxStrips) return W4A16_ERR_TOO_LARGE;
+
+  LinearArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.packed = reinterpret_cast<const uint8_t*>(packed);
+  a.ldp = ldp;
+  a.scale = scale;
+  a.lds = lds;
+  a.y = static_cast<uint16_t*>(y);
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  const bool vw = aligned16(packed) && (ldp % 16 == 0) && aligned16(scale) && (lds % 4 == 0);
+  const bool vx = aligned16(x) && (ldx % 8 == 0);
+  const bool vy = (((uintptr_t)y & 7u) == 0) && (ldy % 4 == 0);
+  a.vec = (vw ? 1 : 0) | (vx ? 2 : 0) | (vy ? 4 : 0);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  if (K == 0) {
+    hipLaunchKernelGGL(zero_kernel, dim3(ceil_div((int64_t)M * N, 256)), dim3(256), 0, s, a.y, ldy, M, N);
+    return launch_status();
+  }
+
+  if (p.kind == 1) {
+    if (!vx) {
+      // The gemm stages activations with 16-byte loads; unaligned activations
+      // are processed 32 rows at a time by the skinny kernel instead.
+      for (int m0 = 0; m0 < M; m0 += 32) {
+        const int mc = M - m0 < 32 ? M - m0 : 32;
+        int rc = w4a16_linear(static_cast<const uint16_t*>(x) + (int64_t)m0 * ldx, ldx, packed, ldp, scale, lds,
+                              static_cast<uint16_t*>(y) + (int64_t)m0 * ldy, ldy, mc, N, K, group_size,
+                              workspace, workspace_bytes, stream);
+        if (rc != W4A16_OK) return rc;
+      }
+      return W4A16_OK;
+    }
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    a.mtiles = ceil_div(M, kGemmRows);
+    a.ntiles = ceil_div(N, kGemmCols);
+    const int64_t items = (int64_t)M * (K / kGroup);
+    hipLaunchKernelGGL(rowsum_kernel, dim3(ceil_div(items, 16)), dim3(256), 0, s, a.x, ldx, M, K, 1, a.part);
+    int rc = launch_status();
+    if (rc != W4A16_OK) return rc;
+    int blocks = a.mtiles * a.ntiles;
+    blocks = (blocks + 7) & ~7;
+    hipLaunchKernelGGL(gemm_kernel, dim3(blocks), dim3(256), 0, s, a);
+    return launch_status();
+  }
+
+  a.gps = p.gps;
+  a.nsplit = p.nsplit;
+  if (p.nsplit > 1) {
+    a.counters = static_cast<uint32_t*>(workspace);
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  }
+  if (p.mt == 1 && p.cpl == 16) return launch_skinny<1, 16>(a, p, s);
+  if (p.mt == 1) return launch_skinny<1, 8>(a, p, s);
+  return launch_skinny<2, 8>(a, p, s);
+}
+
+int w4a16_dequant(const int8_t* packed, int64_t ldp, const float* scale, int64_t lds, void* out, int64_t ldo,
+                  int out_dtype, int K, int N, int group_size, void* stream) {
+  if (K < 0 || N < 0) return W4A16_ERR_SHAPE;
+  if (group_size <= 0) return W4A16_ERR_GROUP_SIZE;
+  if (K % group_size != 0 || K % 2 != 0) return W4A16_ERR_K_GROUP;
+  if (out_dtype != W4A16_DTYPE_F32 && out_dtype != W4A16_DTYPE_BF16) return W4A16_ERR_DTYPE;
+  if (K == 0 || N == 0) return W4A16_OK;
+  if (!packed || !scale || !out) return W4A16_ERR_NULL;
+  if (ldp < N || lds < N || ldo < N) return W4A16_ERR_SHAPE;
+  const int64_t total = (int64_t)(K / 2) * N;
+  hipLaunchKernelGGL(dequant_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     reinterpret_cast<const uint8_t*>(packed), ldp, scale, lds, out, ldo,
+                     out_dtype == W4A16_DTYPE_BF16 ? 1 : 0, K, N, group_size);
+  return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,22 @@
+"""w4a16 -- MI355X-native INT4-weight / bf16-activation linear.
+
+Drop-in for the INT4 surface of waleedalfar/inf-engine: ``int4_matmul`` and the
+format helpers of engine/kernels/quant.py, ``_Int4Weight`` / ``quantize_llama``
+of engine/quantize.py and ``linear`` of engine/layers.py.  The contraction runs
+in hand-written gfx950 HIP kernels behind the C ABI of include/w4a16.h.
+"""
+
+from .layers import linear
+from .quant import dequantize_weight_int4, int4_matmul, quantize_weight_int4
+from .quantize import QuantizedLlamaWeights, _Int4Weight, quantize_llama, quantized_to_device
+
+__all__ = [
+    "linear",
+    "int4_matmul",
+    "quantize_weight_int4",
+    "dequantize_weight_int4",
+    "quantize_llama",
+    "quantized_to_device",
+    "QuantizedLlamaWeights",
+    "_Int4Weight",
+]

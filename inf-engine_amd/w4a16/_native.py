@@ -1,0 +1,180 @@
+"""ctypes binding of the C ABI declared in include/w4a16.h.
+
+The shared library ``libw4a16.so`` is built in-tree (see ``w4a16.build``) and
+loaded from this package directory.  There is no fallback: if the library is
+missing or a HIP device is absent, every device entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libw4a16.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+W4A16_OK = 0
+W4A16_ERR_NULL = 1
+W4A16_ERR_SHAPE = 2
+W4A16_ERR_K_GROUP = 3
+W4A16_ERR_GROUP_SIZE = 4
+W4A16_ERR_WORKSPACE = 5
+W4A16_ERR_LAUNCH = 6
+W4A16_ERR_DTYPE = 7
+W4A16_ERR_TOO_LARGE = 8
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+# Every symbol include/w4a16.h declares.
+EXPORTED_SYMBOLS = (
+    "w4a16_abi_version",
+    "w4a16_error_string",
+    "w4a16_workspace_size",
+    "w4a16_linear",
+    "w4a16_dequant",
+)
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+class NativeLibraryMissing(RuntimeError):
+    """The HIP extension has not been built (run ``__graft_entry__.build()``)."""
+
+
+def load_library() -> ctypes.CDLL:
+    """Load (once) and return the native library, with argtypes configured."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise NativeLibraryMissing(
+                f"{LIB_PATH} not found: the w4a16 HIP extension is not built "
+                "(python -c 'import __graft_entry__ as g; g.build()')"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        i64, i32, vp, sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
+        lib.w4a16_abi_version.argtypes = []
+        lib.w4a16_abi_version.restype = i32
+        lib.w4a16_error_string.argtypes = [i32]
+        lib.w4a16_error_string.restype = ctypes.c_char_p
+        lib.w4a16_workspace_size.argtypes = [i32, i32, i32, i32, ctypes.POINTER(sz)]
+        lib.w4a16_workspace_size.restype = i32
+        lib.w4a16_linear.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp, sz, vp]
+        lib.w4a16_linear.restype = i32
+        lib.w4a16_dequant.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
+        lib.w4a16_dequant.restype = i32
+        _lib = lib
+        return lib
+
+
+def error_string(code: int) -> str:
+    return load_library().w4a16_error_string(code).decode()
+
+
+def check(code: int, what: str) -> None:
+    """Map a C status to the exception type the reference raises for it."""
+    if code == W4A16_OK:
+        return
+    msg = f"{what}: {error_string(code)} (code {code})"
+    if code == W4A16_ERR_GROUP_SIZE:
+        # engine/kernels/quant.py:267 asserts group_size == 128.
+        raise AssertionError(msg)
+    if code in (W4A16_ERR_K_GROUP, W4A16_ERR_SHAPE):
+        # engine/kernels/quant.py:100-103 raise ValueError for bad K.
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def workspace_size(m: int, n: int, k: int, group_size: int = 128) -> int:
+    out = ctypes.c_size_t(0)
+    check(load_library().w4a16_workspace_size(m, n, k, group_size, ctypes.byref(out)), "w4a16_workspace_size")
+    return out.value
+
+
+# One zeroed workspace per (device, stream).  The head of a workspace holds
+# split-K arrival counters that every call leaves at zero, so a buffer is only
+# zeroed when it is (re)allocated.  Calls on one stream are ordered, which is
+# what makes sharing the buffer safe.
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_ws_lock = threading.Lock()
+
+
+def get_workspace(device: torch.device, stream_handle: int, nbytes: int) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_handle)
+    with _ws_lock:
+        ws = _workspaces.get(key)
+        if ws is not None and ws.numel() >= nbytes:
+            return ws
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                "w4a16: the split-K workspace must exist before HIP graph capture; run the "
+                "captured shapes once eagerly on the capture stream first (the reference's "
+                "graph capture also warms up before capturing, llama_paged_engine.py:315-347)"
+            )
+        size = max(nbytes, 1 << 20)
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+        return ws
+
+
+def linear(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_size: int) -> torch.Tensor:
+    """y = a @ dequant(packed, scale) on the current HIP stream; a is [M, K] bf16."""
+    lib = load_library()
+    m, k = a.shape
+    n = packed.shape[1]
+    if a.stride(1) != 1:
+        a = a.contiguous()
+    if packed.stride(1) != 1:
+        packed = packed.contiguous()
+    if scale.stride(1) != 1:
+        scale = scale.contiguous()
+    y = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream(a.device).cuda_stream
+    nbytes = workspace_size(m, n, k, group_size)
+    ws = get_workspace(a.device, stream, nbytes)
+    rc = lib.w4a16_linear(
+        a.data_ptr(), a.stride(0),
+        packed.data_ptr(), packed.stride(0),
+        scale.data_ptr(), scale.stride(0),
+        y.data_ptr(), y.stride(0),
+        m, n, k, group_size,
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+        stream,
+    )
+    check(rc, "w4a16_linear")
+    return y
+
+
+def dequant(packed: torch.Tensor, scale: torch.Tensor, group_size: int, out_dtype: torch.dtype) -> torch.Tensor:
+    """Dense [K, N] weights from packed/scale on the current HIP stream."""
+    lib = load_library()
+    if out_dtype == torch.float32:
+        code = DTYPE_F32
+    elif out_dtype == torch.bfloat16:
+        code = DTYPE_BF16
+    else:
+        raise TypeError(f"w4a16 dequant supports float32 and bfloat16 outputs, got {out_dtype}")
+    if packed.stride(1) != 1:
+        packed = packed.contiguous()
+    if scale.stride(1) != 1:
+        scale = scale.contiguous()
+    k = packed.shape[0] * 2
+    n = packed.shape[1]
+    out = torch.empty((k, n), device=packed.device, dtype=out_dtype)
+    stream = torch.cuda.current_stream(packed.device).cuda_stream
+    rc = lib.w4a16_dequant(
+        packed.data_ptr(), packed.stride(0), scale.data_ptr(), scale.stride(0),
+        out.data_ptr(), out.stride(0), code, k, n, group_size, stream,
+    )
+    check(rc, "w4a16_dequant")
+    return out

@@ -1,0 +1,138 @@
+"""INT4 W4A16 weight format and fused matmul -- the surface of engine/kernels/quant.py.
+
+Same names, arguments, layouts and error types as the reference module's INT4
+half (engine/kernels/quant.py:77-281):
+
+* ``quantize_weight_int4(w, group_size)``  -> ``(packed[K/2, N] int8, scale[K/g, N])``
+* ``dequantize_weight_int4(packed, scale, group_size)`` -> ``w[K, N]`` in ``scale.dtype``
+* ``int4_matmul(a, packed, scale, group_size=128)`` -> ``a @ w`` in bf16
+
+``int4_matmul`` and device-tensor ``dequantize_weight_int4`` run the gfx950 HIP
+kernels of ``libw4a16.so`` through the C ABI; there is no Triton and no other
+backend.  ``int4_matmul`` refuses host tensors instead of computing on the CPU.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native
+
+_INT4_MAX = 7        # symmetric code range [-7, 7] produced by the quantizer
+_NIBBLES_PER_BYTE = 2
+FUSED_GROUP_SIZE = 128
+
+
+def quantize_weight_int4(w: torch.Tensor, group_size: int = 128) -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric per-group INT4 quantization of a ``(d_in, d_out)`` weight.
+
+    Follows engine/kernels/quant.py:81-119 operation for operation, so the
+    packed bytes and scales are bit-identical to the reference's on the same
+    input: per (group, column) ``scale = max(amax|w| / 7, 1e-8)``, codes
+    ``clamp(round_half_even(w / scale), -7, 7)``, and rows ``2i`` / ``2i+1``
+    packed into the high / low nibble of byte ``i``.
+
+    This is one-time weight preparation in torch on whatever device ``w`` lives
+    (the reference does the same, engine/quantize.py:187-188); it is not the
+    measured path.
+
+    Raises:
+        ValueError: ``d_in`` not divisible by ``group_size`` or odd.
+    """
+    d_in, d_out = w.shape
+    if d_in % group_size != 0:
+        raise ValueError(f"d_in={d_in} not divisible by group_size={group_size}")
+    if d_in % _NIBBLES_PER_BYTE != 0:
+        raise ValueError(f"d_in={d_in} must be even for nibble packing")
+    groups = d_in // group_size
+    grouped = w.reshape(groups, group_size, d_out)
+    scale = (grouped.abs().amax(dim=1) / _INT4_MAX).clamp(min=1e-8)          # (G, d_out)
+    codes = (grouped / scale[:, None, :].expand_as(grouped)).round()
+    codes = codes.clamp(-_INT4_MAX, _INT4_MAX).to(torch.int8).reshape(d_in, d_out)
+    hi = (codes[0::2] & 0x0F).to(torch.uint8)
+    lo = (codes[1::2] & 0x0F).to(torch.uint8)
+    packed = ((hi << 4) | lo).to(torch.int8)
+    return packed, scale
+
+
+def _dequantize_host(packed: torch.Tensor, scale: torch.Tensor, group_size: int) -> torch.Tensor:
+    d_half, d_out = packed.shape
+    d_in = d_half * _NIBBLES_PER_BYTE
+    even = packed >> 4                                       # int8 arithmetic shift: sign-extends
+    odd = ((packed & 0x0F).to(torch.int8) << 4) >> 4
+    codes = torch.stack((even, odd), dim=1).reshape(d_in, d_out)
+    groups = d_in // group_size
+    w = codes.reshape(groups, group_size, d_out).to(scale.dtype) * scale[:, None, :]
+    return w.reshape(d_in, d_out)
+
+
+def dequantize_weight_int4(packed: torch.Tensor, scale: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """Unpack INT4 weights to ``(d_in, d_out)`` in ``scale.dtype``.
+
+    Semantics of engine/kernels/quant.py:122-156: even rows come from the high
+    nibble (int8 arithmetic shift), odd rows from the sign-extended low nibble,
+    and row ``k`` is multiplied by ``scale[k // group_size]``.
+
+    Device tensors run the HIP ``w4a16_dequant`` kernel (float32 or bfloat16
+    scales).  Host tensors are unpacked with torch on the host, as the
+    reference does for host tensors; this is a format utility, not the fused
+    contraction.
+    """
+    d_half, d_out = packed.shape
+    d_in = d_half * _NIBBLES_PER_BYTE
+    if group_size <= 0 or d_in % group_size != 0:
+        raise ValueError(f"d_in={d_in} not divisible by group_size={group_size}")
+    if scale.shape != (d_in // group_size, d_out):
+        raise ValueError(f"scale shape {tuple(scale.shape)} != {(d_in // group_size, d_out)}")
+    if not packed.is_cuda:
+        return _dequantize_host(packed, scale, group_size)
+    if scale.device != packed.device:
+        raise ValueError("packed and scale must be on the same device")
+    if scale.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"device dequantize supports float32/bfloat16 scales, got {scale.dtype}")
+    with torch.cuda.device(packed.device):
+        return _native.dequant(packed, scale.float(), group_size, scale.dtype)
+
+
+def int4_matmul(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """Fused W4A16 matmul ``a @ dequantize(packed, scale)`` without a dense weight.
+
+    Drop-in for engine/kernels/quant.py:243-281.  ``a`` is ``(M, K)`` bf16 on a
+    HIP device, ``packed`` ``(K/2, N)`` int8, ``scale`` ``(K/128, N)`` float32.
+    Returns ``(M, N)`` bf16, allocated on the caller's stream; the call
+    enqueues on the current stream and never synchronises, so it can be
+    captured in a HIP graph once its workspace exists.
+
+    M <= 32 runs the HBM-bound skinny kernel, larger M the MFMA GEMM.
+
+    Raises:
+        AssertionError: ``group_size != 128`` (as engine/kernels/quant.py:267).
+        ValueError: inconsistent shapes.
+        TypeError: host tensors or non-bf16 activations.
+    """
+    if not a.is_cuda:
+        raise TypeError(
+            "w4a16.int4_matmul runs only on HIP device tensors; this package has no host "
+            "implementation of the fused contraction"
+        )
+    assert group_size == FUSED_GROUP_SIZE, f"fused INT4 kernel requires group_size=128, got {group_size}"
+    if a.dim() != 2 or packed.dim() != 2 or scale.dim() != 2:
+        raise ValueError("int4_matmul expects a[M,K], packed[K/2,N], scale[K/128,N]")
+    m, k = a.shape
+    k_half, n = packed.shape
+    if k != 2 * k_half:
+        raise ValueError(f"a has K={k} but packed has {k_half} rows (expected K/2)")
+    if k % group_size != 0:
+        raise ValueError(f"K={k} not divisible by group_size={group_size}")
+    if scale.shape != (k // group_size, n):
+        raise ValueError(f"scale shape {tuple(scale.shape)} != {(k // group_size, n)}")
+    if a.dtype != torch.bfloat16:
+        raise TypeError(f"int4_matmul activations must be bfloat16, got {a.dtype}")
+    if packed.dtype not in (torch.int8, torch.uint8):
+        raise TypeError(f"packed weights must be int8, got {packed.dtype}")
+    if packed.device != a.device or scale.device != a.device:
+        raise ValueError("a, packed and scale must be on the same device")
+    if scale.dtype != torch.float32:
+        scale = scale.float()
+    with torch.cuda.device(a.device):
+        return _native.linear(a, packed, scale, group_size)

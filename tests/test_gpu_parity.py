@@ -1,0 +1,333 @@
+"""GPU parity of the HIP W4A16 path against the CPU oracle (run with -m gpu).
+
+Bars (written out in each test):
+* unpack + scale indexing: bit-exact (dequant kernel; one-hot activations
+  through the fused kernels; integer problems with power-of-two scales).
+* fused output: max |y - y_ref| <= 1e-2 * RMS(y_ref) + ulp_bf16(y_ref) / 2,
+  where y_ref is the float64 product of the same packed weights.  The half-ulp
+  term is the bf16 rounding of the output itself, which alone can exceed
+  1e-2 * RMS for |y| above ~2.5 RMS; a second, tighter bar (1e-3 * RMS on top of
+  the half ulp) catches real accumulation errors.
+Full benchmark shapes are checked against an fp32 torch dequantize-then-matmul
+of the same weights on the GPU plus a float64 oracle check on sampled columns.
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import int4_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "int4_golden.npz")
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu(native_lib):
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    torch.backends.cuda.matmul.allow_tf32 = False
+    yield
+
+
+def ulp_bf16(v: np.ndarray) -> np.ndarray:
+    a = np.abs(v).astype(np.float64)
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
+    return np.ldexp(1.0, (e - 7).astype(np.int64))
+
+
+def check_tolerance(y: torch.Tensor, y_ref: np.ndarray, label: str) -> None:
+    yv = y.float().cpu().numpy().astype(np.float64)
+    rms = float(np.sqrt(np.mean(y_ref ** 2)))
+    err = np.abs(yv - y_ref)
+    excess = err - ulp_bf16(y_ref) / 2
+    say(f"  {label}: rms={rms:.4g} max|d|/rms={err.max() / rms:.3e} max(excess)/rms={excess.max() / rms:.3e}")
+    assert np.isfinite(yv).all(), label
+    assert excess.max() <= 1e-2 * rms, label
+    assert excess.max() <= 1e-3 * rms, label
+
+
+def rand_problem(m, k, n, seed, dev=DEV):
+    g = torch.Generator().manual_seed(seed)
+    packed = torch.randint(-128, 128, (k // 2, n), generator=g, dtype=torch.int8)
+    scale = (torch.rand(k // 128, n, generator=g) * 0.01 + 0.001)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    return x.to(dev), packed.to(dev), scale.to(dev)
+
+
+# ---------------------------------------------------------------------------
+# Bit-exact unpack and scale indexing
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("k,n,gs", [(256, 64, 128), (512, 100, 128), (1024, 3072, 128), (256, 33, 64)])
+def test_dequant_bit_exact(k, n, gs):
+    from w4a16 import dequantize_weight_int4
+
+    say(f"dequant k={k} n={n} gs={gs}")
+    g = torch.Generator().manual_seed(k + n)
+    packed = torch.randint(-128, 128, (k // 2, n), generator=g, dtype=torch.int8)
+    scale = torch.randn(k // gs, n, generator=g)
+    out = dequantize_weight_int4(packed.to(DEV), scale.to(DEV), gs)
+    np.testing.assert_array_equal(out.cpu().numpy(), orc.dequantize(packed.numpy(), scale.numpy(), gs))
+    outb = dequantize_weight_int4(packed.to(DEV), scale.to(DEV).bfloat16(), gs)
+    assert outb.dtype == torch.bfloat16
+    np.testing.assert_array_equal(outb.float().cpu().numpy(), orc.dequantize_bf16(packed.numpy(), scale.numpy(), gs))
+
+
+def test_dequant_golden():
+    from w4a16 import dequantize_weight_int4
+
+    g = np.load(GOLDEN)
+    out = dequantize_weight_int4(torch.from_numpy(g["packed"]).to(DEV), torch.from_numpy(g["scale"]).to(DEV))
+    np.testing.assert_array_equal(out.cpu().numpy(), g["dequant"])
+
+
+@pytest.mark.parametrize("m,k,n", [(7, 512, 256), (32, 1024, 4096), (100, 512, 300), (256, 384, 512)])
+def test_one_hot_rows_bit_exact(m, k, n):
+    """x[i] = e_{k_i}: y[i, n] = bf16(fp32(q[k_i, n] * scale[k_i // 128, n])) exactly,
+    through the skinny (M <= 32) and the GEMM (M > 32) kernels."""
+    from w4a16 import int4_matmul
+
+    say(f"one-hot m={m} k={k} n={n}")
+    g = torch.Generator().manual_seed(m * 7 + k)
+    packed = torch.randint(-128, 128, (k // 2, n), generator=g, dtype=torch.int8)
+    scale = torch.randn(k // 128, n, generator=g)
+    rows = torch.randint(0, k, (m,), generator=g)
+    x = torch.zeros(m, k)
+    x[torch.arange(m), rows] = 1.0
+    y = int4_matmul(x.bfloat16().to(DEV), packed.to(DEV), scale.to(DEV))
+    c = orc.codes(packed.numpy())
+    r = rows.numpy()
+    expect = orc.bf16_round(c[r].astype(np.float32) * scale.numpy()[r // 128])
+    np.testing.assert_array_equal(y.float().cpu().numpy(), expect)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 1024), (5, 1024, 512), (33, 1024, 512), (128, 768, 1024)])
+def test_integer_problem_exact(m, k, n):
+    """Integer activations, power-of-two scales: every partial is exact in fp32,
+    so the result must be the bf16 rounding of the exact product."""
+    from w4a16 import int4_matmul
+
+    say(f"integer m={m} k={k} n={n}")
+    rng = np.random.default_rng(m + k + n)
+    packed = rng.integers(0, 256, size=(k // 2, n), dtype=np.uint8).view(np.int8)
+    scale = np.ldexp(np.float32(1.0), rng.integers(-4, 3, size=(k // 128, n))).astype(np.float32)
+    x = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
+    y = int4_matmul(torch.from_numpy(x).bfloat16().to(DEV), torch.from_numpy(packed).to(DEV),
+                    torch.from_numpy(scale).to(DEV))
+    exact = orc.fused_reference(x, packed, scale)
+    np.testing.assert_array_equal(y.float().cpu().numpy(), orc.bf16_round(exact.astype(np.float32)))
+
+
+def test_golden_product():
+    from w4a16 import int4_matmul
+
+    g = np.load(GOLDEN)
+    y = int4_matmul(torch.from_numpy(g["x"]).bfloat16().to(DEV), torch.from_numpy(g["packed"]).to(DEV),
+                    torch.from_numpy(g["scale"]).to(DEV))
+    np.testing.assert_array_equal(y.float().cpu().numpy(), orc.bf16_round(g["y"].astype(np.float32)))
+
+
+# ---------------------------------------------------------------------------
+# Tolerance against the float64 oracle at oracle-sized shapes
+# ---------------------------------------------------------------------------
+
+SHAPES = [
+    # (M, K, N): Qwen3-0.6B gate (config 1), ragged N, M on both sides of 32
+    (1, 1024, 3072), (2, 1024, 3072), (3, 512, 1000), (4, 4096, 1024), (8, 1024, 4096),
+    (16, 2048, 1536), (17, 1024, 2048), (31, 512, 768), (32, 4096, 1024),
+    (33, 1024, 1024), (64, 1024, 1280), (100, 768, 1000), (129, 512, 640), (256, 2048, 1024),
+]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+def test_tolerance_vs_oracle(m, k, n):
+    from w4a16 import int4_matmul, synth
+
+    say(f"tolerance m={m} k={k} n={n}")
+    packed, scale = synth.make_weight(k, n, seed=1000 + n)
+    x = synth.make_activations(m, k, seed=2000 + m)
+    y = int4_matmul(x.to(DEV), packed.to(DEV), scale.to(DEV))
+    assert y.shape == (m, n) and y.dtype == torch.bfloat16
+    y_ref = orc.fused_reference(x.float().numpy(), packed.numpy(), scale.numpy())
+    check_tolerance(y, y_ref, f"M={m} K={k} N={n}")
+
+
+def test_unaligned_and_strided_activations():
+    """Row stride > K, an activation pointer off 16-byte alignment (generic loads),
+    and a transposed view (made contiguous by the wrapper)."""
+    from w4a16 import int4_matmul
+
+    for m in (3, 40):
+        say(f"strided m={m}")
+        x, packed, scale = rand_problem(m, 512, 256, seed=m)
+        y_ref = orc.fused_reference(x.float().cpu().numpy(), packed.cpu().numpy(), scale.cpu().numpy())
+        big = torch.zeros(m, 512 + 8, dtype=torch.bfloat16, device=DEV)
+        big[:, :512] = x
+        check_tolerance(int4_matmul(big[:, :512], packed, scale), y_ref, f"ldx=520 M={m}")
+        flat = torch.zeros(m * 512 + 1, dtype=torch.bfloat16, device=DEV)
+        xu = flat[1:].view(m, 512)
+        xu.copy_(x)
+        check_tolerance(int4_matmul(xu, packed, scale), y_ref, f"unaligned M={m}")
+        xt = x.t().contiguous().t()
+        check_tolerance(int4_matmul(xt, packed, scale), y_ref, f"transposed M={m}")
+
+
+def test_empty_and_zero_k():
+    from w4a16 import int4_matmul
+
+    _, packed, scale = rand_problem(1, 256, 64, seed=3)
+    y = int4_matmul(torch.empty(0, 256, dtype=torch.bfloat16, device=DEV), packed, scale)
+    assert y.shape == (0, 64)
+    y = int4_matmul(torch.empty(4, 0, dtype=torch.bfloat16, device=DEV),
+                    torch.empty(0, 64, dtype=torch.int8, device=DEV), torch.empty(0, 64, device=DEV))
+    assert y.shape == (4, 64) and torch.count_nonzero(y) == 0
+    y = int4_matmul(torch.empty(40, 0, dtype=torch.bfloat16, device=DEV),
+                    torch.empty(0, 64, dtype=torch.int8, device=DEV), torch.empty(0, 64, device=DEV))
+    assert y.shape == (40, 64) and torch.count_nonzero(y) == 0
+
+
+def test_errors_on_device():
+    from w4a16 import int4_matmul
+
+    x, packed, scale = rand_problem(2, 256, 64, seed=4)
+    with pytest.raises(AssertionError):
+        int4_matmul(x, packed, scale, group_size=64)
+    with pytest.raises(ValueError):
+        int4_matmul(x[:, :128], packed, scale)
+    with pytest.raises(TypeError):
+        int4_matmul(x.float(), packed, scale)
+
+
+def test_fused_linear_reshapes_leading_dims():
+    from w4a16 import _Int4Weight, linear, synth
+
+    packed, scale = synth.make_weight(512, 384, seed=9)
+    w4 = _Int4Weight(packed.to(DEV), scale.to(DEV), 128, (384, 512))
+    x = synth.make_activations(6, 512, seed=10).reshape(2, 3, 512)
+    y = linear(x.to(DEV), w4)
+    assert y.shape == (2, 3, 384)
+    y_ref = orc.fused_reference(x.reshape(6, 512).float().numpy(), packed.numpy(), scale.numpy())
+    check_tolerance(y.reshape(6, 384), y_ref, "fused_linear [2,3,512]")
+    dense = w4.dequantize(torch.float32)
+    np.testing.assert_array_equal(dense.cpu().numpy(), orc.dequantize(packed.numpy(), scale.numpy()).T)
+
+
+def test_split_k_deterministic_and_counters_reset():
+    """Repeated and interleaved calls sharing one workspace give identical bits."""
+    from w4a16 import int4_matmul
+
+    probs = [rand_problem(m, k, n, seed=m + k) for (m, k, n) in [(1, 4096, 12288), (4, 12288, 4096), (16, 4096, 1024)]]
+    first = [int4_matmul(*p) for p in probs]
+    for _ in range(3):
+        for p, y0 in zip(probs, first):
+            assert torch.equal(int4_matmul(*p), y0)
+
+
+def test_quantize_llama_on_device_matches_dense():
+    """quantize_llama -> quantized_to_device -> linear: matches dequantize-then-matmul."""
+    from w4a16 import linear, quantize_llama, quantized_to_device
+    from test_host import _mini_model
+
+    model, _ = _mini_model(d=512, f=768, layers=1, kv=256)
+    q_model = quantized_to_device(quantize_llama(model, 128), DEV)
+    blk = q_model.w.layer(0)
+    x = torch.randn(5, 512).bfloat16()
+    for suffix in ("self_attn.q_proj.weight", "mlp.gate_proj.weight"):
+        w4 = blk[suffix]
+        y = linear(x.to(DEV), w4)
+        y_ref = orc.fused_reference(x.float().numpy(), w4.packed.cpu().numpy(), w4.scale.cpu().numpy())
+        check_tolerance(y, y_ref, suffix)
+    # down_proj: K = 768
+    w4 = blk["mlp.down_proj.weight"]
+    x = torch.randn(40, 768).bfloat16()
+    y = linear(x.to(DEV), w4)
+    check_tolerance(y, orc.fused_reference(x.float().numpy(), w4.packed.cpu().numpy(), w4.scale.cpu().numpy()),
+                    "down_proj M=40")
+
+
+def test_graph_capture_replays_match_eager():
+    """int4_matmul captured in a HIP graph: each replay, separated by eager work
+    and synchronisation, must reproduce the eager result bit for bit."""
+    from w4a16 import int4_matmul
+
+    cases = [rand_problem(m, k, n, seed=50 + m) for (m, k, n) in [(1, 4096, 12288), (8, 4096, 1024), (64, 1024, 2048)]]
+    eager = [int4_matmul(*c) for c in cases]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for c in cases:   # warm up on the capture stream: creates its workspace
+            int4_matmul(*c)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        outs = [int4_matmul(*c) for c in cases]
+    for rep in range(4):
+        for o in outs:
+            o.zero_()
+        junk = torch.randn(1024, 1024, device=DEV) @ torch.randn(1024, 1024, device=DEV)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {rep}"
+        del junk
+
+
+# ---------------------------------------------------------------------------
+# Benchmark configs at full size
+# ---------------------------------------------------------------------------
+
+def full_size_check(m, k, n, seed, label):
+    from w4a16 import dequantize_weight_int4, int4_matmul, synth
+
+    say(f"full-size {label}: M={m} K={k} N={n}")
+    packed, scale = synth.make_weight(k, n, seed=seed, device=DEV)
+    x = synth.make_activations(m, k, seed=seed + 1, device=DEV)
+    y = int4_matmul(x, packed, scale)
+    w = dequantize_weight_int4(packed, scale)                    # bit-exact (tested above)
+    y_ref = (x.float() @ w).double().cpu().numpy()                # fp32 dequantize-then-matmul
+    check_tolerance(y, y_ref, label)
+    # float64 oracle on sampled columns
+    cols = torch.randperm(n, generator=torch.Generator().manual_seed(seed))[:48].sort().values
+    y64 = orc.fused_reference(x.float().cpu().numpy(), packed[:, cols.to(DEV)].cpu().numpy(),
+                              scale[:, cols.to(DEV)].cpu().numpy())
+    check_tolerance(y[:, cols.to(DEV)], y64, label + " (fp64 oracle, 48 cols)")
+    del w
+
+
+@pytest.mark.parametrize("name,k,n", [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
+                                      ("gate", 4096, 12288), ("up", 4096, 12288), ("down", 12288, 4096)])
+def test_config2_qwen3_8b_decode(name, k, n):
+    full_size_check(1, k, n, seed=sum(map(ord, name)), label=f"qwen3-8b {name} M=1")
+
+
+@pytest.mark.parametrize("m", [4, 8, 16, 32])
+@pytest.mark.parametrize("k,n", [(4096, 12288), (12288, 4096)])
+def test_config3_qwen3_8b_batched(m, k, n):
+    full_size_check(m, k, n, seed=m * 31 + k, label=f"qwen3-8b M={m} {k}x{n}")
+
+
+@pytest.mark.parametrize("name,k,n", [("q", 4096, 4096), ("k", 4096, 1024), ("o", 4096, 4096),
+                                      ("gate", 4096, 12288), ("down", 12288, 4096)])
+def test_config4_qwen3_8b_prefill(name, k, n):
+    full_size_check(2048, k, n, seed=len(name) * 97 + k, label=f"qwen3-8b {name} M=2048")
+
+
+@pytest.mark.parametrize("name,m,k,n", [("q", 1, 5120, 8192), ("kv", 1, 5120, 1024), ("o", 1, 8192, 5120),
+                                        ("gate", 1, 5120, 25600), ("down", 1, 25600, 5120),
+                                        ("gate", 4096, 5120, 25600), ("down", 4096, 25600, 5120)])
+def test_config5_qwen3_32b(name, m, k, n):
+    full_size_check(m, k, n, seed=m + k + n, label=f"qwen3-32b {name} M={m}")

@@ -1,0 +1,223 @@
+"""Host-side checks that need no GPU: the C ABI library, argument validation,
+workspace planning and the Python surface (quantize_llama, error mapping)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import int4_oracle as orc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "w4a16.h")
+
+
+def header_functions() -> list[str]:
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(w4a16_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol(native_lib):
+    from w4a16 import _native
+
+    names = header_functions()
+    assert set(names) == set(_native.EXPORTED_SYMBOLS), names
+    for name in names:
+        assert hasattr(native_lib, name), name
+    assert native_lib.w4a16_abi_version() == 1
+
+
+def _linear(lib, *, x=1, ldx=4096, packed=1, ldp=4096, scale=1, lds=4096, y=1, ldy=4096, m=1, n=4096,
+            k=4096, gs=128, ws=None, ws_bytes=0):
+    return lib.w4a16_linear(x, ldx, packed, ldp, scale, lds, y, ldy, m, n, k, gs, ws, ws_bytes, None)
+
+
+def test_linear_argument_validation_returns_codes(native_lib):
+    from w4a16 import _native as nat
+
+    lib = native_lib
+    assert _linear(lib, gs=64) == nat.W4A16_ERR_GROUP_SIZE
+    assert _linear(lib, k=200, ldx=200) == nat.W4A16_ERR_K_GROUP
+    assert _linear(lib, m=-1) == nat.W4A16_ERR_SHAPE
+    assert _linear(lib, ldx=100) == nat.W4A16_ERR_SHAPE
+    assert _linear(lib, ldp=100) == nat.W4A16_ERR_SHAPE
+    assert _linear(lib, lds=100) == nat.W4A16_ERR_SHAPE
+    assert _linear(lib, ldy=100) == nat.W4A16_ERR_SHAPE
+    assert _linear(lib, x=None) == nat.W4A16_ERR_NULL
+    assert _linear(lib, packed=None) == nat.W4A16_ERR_NULL
+    assert _linear(lib, scale=None) == nat.W4A16_ERR_NULL
+    assert _linear(lib, y=None) == nat.W4A16_ERR_NULL
+    # Split-K shapes need a workspace: rejected before anything is launched.
+    assert _linear(lib, n=12288, ldp=12288, lds=12288, ldy=12288) == nat.W4A16_ERR_WORKSPACE
+    # Empty outputs are no-ops that touch no pointer.
+    assert _linear(lib, m=0, x=None, packed=None, scale=None, y=None) == nat.W4A16_OK
+    assert _linear(lib, n=0, x=None, packed=None, scale=None, y=None) == nat.W4A16_OK
+
+
+def test_dequant_argument_validation(native_lib):
+    from w4a16 import _native as nat
+
+    lib = native_lib
+    assert lib.w4a16_dequant(1, 8, 1, 8, 1, 8, 5, 256, 8, 128, None) == nat.W4A16_ERR_DTYPE
+    assert lib.w4a16_dequant(1, 8, 1, 8, 1, 8, 0, 256, 8, 0, None) == nat.W4A16_ERR_GROUP_SIZE
+    assert lib.w4a16_dequant(1, 8, 1, 8, 1, 8, 0, 250, 8, 128, None) == nat.W4A16_ERR_K_GROUP
+    assert lib.w4a16_dequant(None, 8, 1, 8, 1, 8, 0, 256, 8, 128, None) == nat.W4A16_ERR_NULL
+    assert lib.w4a16_dequant(1, 4, 1, 8, 1, 8, 0, 256, 8, 128, None) == nat.W4A16_ERR_SHAPE
+    assert lib.w4a16_dequant(None, 8, None, 8, None, 8, 0, 0, 8, 128, None) == nat.W4A16_OK
+
+
+def test_error_strings(native_lib):
+    for code in range(9):
+        assert native_lib.w4a16_error_string(code)
+    assert b"128" in native_lib.w4a16_error_string(4)
+
+
+def test_workspace_planning(native_lib):
+    from w4a16 import _native
+
+    ws = _native.workspace_size
+    assert ws(0, 4096, 4096) == 0
+    assert ws(1, 0, 4096) == 0
+    # M=1 Qwen3-8B gate: split-K partials (fp32 [splits, 1, N]) after 64 KiB of counters.
+    b = ws(1, 12288, 4096)
+    assert b > 65536 and (b - 65536) % (12288 * 4) == 0
+    # Large M: per-(group, row) correction sums.
+    assert ws(2048, 12288, 4096) == 65536 + 32 * 2048 * 4
+    with pytest.raises(AssertionError):
+        ws(1, 4096, 4096, 64)
+    with pytest.raises(ValueError):
+        ws(1, 4096, 4000)
+    # Split count never gives a wave no group and never exceeds the K groups.
+    for m in (1, 2, 4, 8, 16, 17, 32):
+        for k in (128, 1024, 4096, 12288, 25600):
+            for n in (64, 1000, 1024, 12288):
+                b = ws(m, n, k)
+                if b:
+                    splits = (b - 65536) // (m * n * 4)
+                    assert 2 <= splits <= (k // 128 + 3) // 4
+
+
+def test_int4_matmul_rejects_host_tensors_and_bad_args():
+    from w4a16 import int4_matmul
+
+    a = torch.randn(2, 256, dtype=torch.bfloat16)
+    packed = torch.zeros(128, 64, dtype=torch.int8)
+    scale = torch.ones(2, 64)
+    with pytest.raises(TypeError):
+        int4_matmul(a, packed, scale)
+
+
+def test_quantize_matches_oracle_bit_exact():
+    from w4a16 import quantize_weight_int4
+
+    torch.manual_seed(4)
+    for d_in, d_out, gs in [(256, 96, 128), (1024, 40, 64), (4096, 16, 128)]:
+        w = (torch.randn(d_in, d_out) * 0.02).to(torch.bfloat16).float()
+        p, s = quantize_weight_int4(w, gs)
+        po, so = orc.quantize(w.numpy(), gs)
+        np.testing.assert_array_equal(p.numpy(), po)
+        np.testing.assert_array_equal(s.numpy(), so)
+    with pytest.raises(ValueError):
+        quantize_weight_int4(torch.randn(100, 8), 128)
+    with pytest.raises(ValueError):
+        quantize_weight_int4(torch.randn(129, 8), 129)
+
+
+def test_host_dequantize_matches_oracle():
+    from w4a16 import dequantize_weight_int4
+
+    g = np.load(os.path.join(ROOT, "tests", "golden", "int4_golden.npz"))
+    out = dequantize_weight_int4(torch.from_numpy(g["packed"]), torch.from_numpy(g["scale"]), 128)
+    np.testing.assert_array_equal(out.numpy(), g["dequant"])
+    outb = dequantize_weight_int4(torch.from_numpy(g["packed"]), torch.from_numpy(g["scale"]).bfloat16(), 128)
+    np.testing.assert_array_equal(outb.float().numpy(), orc.dequantize_bf16(g["packed"], g["scale"]))
+
+
+class _MiniWeights:
+    """Just enough of the reference's LlamaWeights (engine/llama_weights.py) for quantize_llama."""
+
+    def __init__(self, tensors, config):
+        self._t = tensors
+        self.config = config
+
+    @property
+    def embed_tokens(self):
+        return self._t["model.embed_tokens.weight"]
+
+    @property
+    def lm_head(self):
+        return self._t["model.embed_tokens.weight"]
+
+    @property
+    def norm_weight(self):
+        return self._t["model.norm.weight"]
+
+    def layer(self, i):
+        p = f"model.layers.{i}."
+        return {k[len(p):]: v for k, v in self._t.items() if k.startswith(p)}
+
+
+def _mini_model(d=256, f=384, layers=2, kv=128):
+    torch.manual_seed(42)
+    cfg = types.SimpleNamespace(n_layer=layers, is_moe=False, n_experts=0)
+    t = {"model.embed_tokens.weight": torch.randn(64, d), "model.norm.weight": torch.ones(d)}
+    for i in range(layers):
+        p = f"model.layers.{i}."
+        t.update({
+            p + "input_layernorm.weight": torch.ones(d),
+            p + "self_attn.q_proj.weight": torch.randn(d, d),
+            p + "self_attn.k_proj.weight": torch.randn(kv, d),
+            p + "self_attn.v_proj.weight": torch.randn(kv, d),
+            p + "self_attn.o_proj.weight": torch.randn(d, d),
+            p + "mlp.gate_proj.weight": torch.randn(f, d),
+            p + "mlp.up_proj.weight": torch.randn(f, d),
+            p + "mlp.down_proj.weight": torch.randn(d, f),
+        })
+    model = types.SimpleNamespace(config=cfg, w=_MiniWeights(t, cfg), rope_cos=torch.ones(4), rope_sin=torch.zeros(4))
+    return model, {k: v.clone() for k, v in t.items()}
+
+
+def test_quantize_llama_structure_and_values():
+    from w4a16 import QuantizedLlamaWeights, _Int4Weight, linear, quantize_llama
+
+    model, dense = _mini_model()
+    q_model = quantize_llama(model, group_size=128)
+    assert isinstance(q_model.w, QuantizedLlamaWeights)
+    assert q_model.rope_cos is model.rope_cos
+    for i in range(2):
+        blk = q_model.w.layer(i)
+        assert torch.equal(blk["input_layernorm.weight"], dense[f"model.layers.{i}.input_layernorm.weight"])
+        for suffix in ("self_attn.q_proj.weight", "self_attn.k_proj.weight", "mlp.down_proj.weight"):
+            w4 = blk[suffix]
+            assert isinstance(w4, _Int4Weight)
+            w = dense[f"model.layers.{i}.{suffix}"]
+            assert w4.shape == tuple(w.shape)
+            d_out, d_in = w.shape
+            assert w4.packed.shape == (d_in // 2, d_out) and w4.packed.dtype == torch.int8
+            assert w4.scale.shape == (d_in // 128, d_out) and w4.scale.dtype == torch.float32
+            po, so = orc.quantize(w.T.contiguous().float().numpy(), 128)
+            np.testing.assert_array_equal(w4.packed.numpy(), po)
+            np.testing.assert_array_equal(w4.scale.numpy(), so)
+            np.testing.assert_array_equal(w4.dequantize(torch.float32).numpy(), orc.dequantize(po, so).T)
+            # Dense keys were released from the original weights.
+            assert f"model.layers.{i}.{suffix}" not in model.w._t
+    # layers.linear duck-types: dense tensors take a plain matmul, INT4 the HIP path.
+    x = torch.randn(3, 64)
+    wd = torch.randn(32, 64)
+    assert torch.equal(linear(x, wd), x @ wd.T)
+    with pytest.raises(TypeError):
+        linear(torch.randn(1, 256, dtype=torch.bfloat16), q_model.w.layer(0)["self_attn.q_proj.weight"])
+
+
+def test_quantized_to_device_requires_quantized_model():
+    from w4a16 import quantized_to_device
+
+    model, _ = _mini_model(layers=1)
+    with pytest.raises(TypeError):
+        quantized_to_device(model, "cpu")
