@@ -26,6 +26,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "../../include/w4a16.h"
 
@@ -61,7 +62,23 @@ struct LinearArgs {
   int vec;             // bit 0: packed/scale rows 16B aligned; bit 1: x rows 16B aligned;
                        // bit 2: y rows 8B aligned
   int mtiles, ntiles;  // gemm tile grid
+#ifdef W4A16_EXP
+  uint64_t* trace;     // per-wave phase timestamps (experiments only)
+#endif
 };
+
+#ifdef W4A16_EXP
+#define W4A16_MARK(i)                                                                                       \
+  do {                                                                                                      \
+    if (a.trace && (threadIdx.x & 63) == 0)                                                                 \
+      a.trace[(((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6)) * 8 + \
+              (i)] = __builtin_amdgcn_s_memrealtime();                                                      \
+  } while (0)
+#else
+#define W4A16_MARK(i) \
+  do {                \
+  } while (0)
+#endif
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float((uint32_t)h << 16);
@@ -113,12 +130,35 @@ __device__ __forceinline__ uint32_t pair_dyn(Prep w, int c) {
   }
 }
 
+// Raw buffer resource over [base, base + bytes): untyped dword loads
+// (DATA_FORMAT 32 in the third descriptor word), no stride.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int BYTES>
+__device__ __forceinline__ void buffer_load_packed(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                                   uint32_t (&out)[BYTES / 4]) {
+  if constexpr (BYTES == 16) {
+    const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+    out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
+  } else if constexpr (BYTES == 8) {
+    const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+    out[0] = v[0]; out[1] = v[1];
+  } else {
+    out[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+  }
+}
+
 // Load `bytes` (4, 8 or 16) consecutive packed bytes starting at column `col`
 // of one packed row.  Columns at or beyond N read as 0 (q = 0).
-template <int BYTES>
+// FULL: the caller guarantees the whole tile is in bounds and aligned, so the
+// load is unconditional (no per-lane branch; all loads of a group can be in
+// flight together).
+template <int BYTES, bool FULL>
 __device__ __forceinline__ void load_packed(const uint8_t* row, int col, int N, bool vec,
                                             uint32_t (&out)[BYTES / 4]) {
-  if (vec && col + BYTES <= N) {
+  if (FULL || (vec && col + BYTES <= N)) {
     if constexpr (BYTES == 16) {
       u32x4_t v = *reinterpret_cast<const u32x4_t*>(row + col);
       out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
@@ -144,9 +184,9 @@ __device__ __forceinline__ void load_packed(const uint8_t* row, int col, int N, 
 }
 
 // Load `CNT` consecutive fp32 scales from column `col`; columns >= N read 0.
-template <int CNT>
+template <int CNT, bool FULL>
 __device__ __forceinline__ void load_scales(const float* row, int col, int N, bool vec, float (&s)[CNT]) {
-  if (vec && col + CNT <= N) {
+  if (FULL || (vec && col + CNT <= N)) {
 #pragma unroll
     for (int i = 0; i < CNT; i += 4) {
       f32x4_t v = *reinterpret_cast<const f32x4_t*>(row + col + i);
@@ -167,6 +207,103 @@ __device__ __forceinline__ bf16x8_t load_x8(const uint16_t* p, bool vec) {
   return as_bf16x8(v);
 }
 
+template <int CPL>
+struct DecodeSlot {
+  static constexpr int WPR = CPL / 4;
+  uint32_t raw[4][4][WPR];
+  float s[CPL];
+};
+
+// xs: LDS activations [M][kpitch] bf16; g_local = group index within the staged K range.
+template <int CPL>
+__device__ __forceinline__ void decode_compute(const DecodeSlot<CPL>& d, const uint16_t* xs, int kpitch, int g_local,
+                                               int xrow_idx, int lk, uint32_t keep, f32x4_t (&total)[CPL]) {
+  constexpr int WPR = CPL / 4;
+  const bf16x8_t neg136 = as_bf16x8(u32x4_t{kBf16Neg136, kBf16Neg136, kBf16Neg136, kBf16Neg136});
+  const uint16_t* xrow = xs + xrow_idx * kpitch + g_local * kGroup + lk * 8;
+  bf16x8_t A[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xrow + st * 32);
+    A[st] = as_bf16x8(v & keep);
+  }
+  f32x4_t cinit = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < 4; ++st) cinit = mfma16(A[st], neg136, cinit);
+  f32x4_t acc[CPL];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+#pragma unroll
+    for (int wi = 0; wi < WPR; ++wi) {
+      Prep pw[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pw[r] = prep(d.raw[st][r][wi]);
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) {
+        const int t = wi * 4 + c4;
+        const bf16x8_t B = as_bf16x8(u32x4_t{pair_dyn(pw[0], c4), pair_dyn(pw[1], c4),
+                                             pair_dyn(pw[2], c4), pair_dyn(pw[3], c4)});
+        acc[t] = mfma16(A[st], B, st == 0 ? cinit : acc[t]);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < CPL; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) total[t][r] = __builtin_fmaf(acc[t][r], d.s[t], total[t][r]);
+}
+
+// ---------------------------------------------------------------------------
+// Split-K finish shared by the M <= 32 kernels.  Each workgroup publishes its
+// fp32 partial for (split, strip) with agent-scope relaxed atomic stores, which
+// the hardware keeps coherent per access across the XCD L2s (no whole-L2
+// writeback / invalidate as a release/acquire fence would need).  The
+// workgroup barrier waits until those stores are acknowledged before thread 0
+// bumps the strip's arrival counter; the last arrival, whose counter update
+// has returned before it issues any load, sums all partials in split order
+// (deterministic), writes bf16 and resets the counter to zero.  Partials are
+// loaded 8 at a time so their latencies overlap.
+// ---------------------------------------------------------------------------
+template <int NT, class PartialFn>
+__device__ __forceinline__ void splitk_finish(const LinearArgs& a, int strip, int n0, int wcols, int rows,
+                                              PartialFn partial) {
+  const int M = a.M, N = a.N;
+  const int elems = rows * wcols;
+  float* part = a.part + (size_t)blockIdx.y * M * N;
+  for (int e = threadIdx.x; e < elems; e += NT) {
+    const int m = e / wcols, c = e % wcols, n = n0 + c;
+    if (n < N) __hip_atomic_store(part + (size_t)m * N + n, partial(e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  __shared__ int is_last;
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(a.counters + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (prev == (uint32_t)(a.nsplit - 1));
+  }
+  __syncthreads();
+  if (!is_last) return;
+  for (int e = threadIdx.x; e < elems; e += NT) {
+    const int m = e / wcols, c = e % wcols, n = n0 + c;
+    if (n < N) {
+      const float* src = a.part + (size_t)m * N + n;
+      const size_t stride = (size_t)M * N;
+      float v = 0.f;
+      for (int sp0 = 0; sp0 < a.nsplit; sp0 += 8) {
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          t[i] = sp0 + i < a.nsplit ? __hip_atomic_load(src + (size_t)(sp0 + i) * stride, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT)
+                                    : 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v += t[i];
+      }
+      a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(v);
+    }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(a.counters + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------------------
 // Skinny kernel (M <= 32).
 //
@@ -181,18 +318,111 @@ __device__ __forceinline__ bf16x8_t load_x8(const uint16_t* p, bool vec) {
 //
 // Per group g and M-subtile:  acc = -136*sum_k x  (4 MFMAs against a -136 matrix),
 // acc += x . (q + 136) over the 4 K steps, total += acc * scale[g, n].
+// A wave keeps the next group's loads in flight while it computes the current
+// one.
 //
-// The 4 waves of a workgroup split the workgroup's groups round-robin and are
-// summed through LDS.  Workgroups along gridDim.y split K further; each writes
-// an fp32 partial and the last one to arrive for a column strip (arrival
+// The WAVES waves of a workgroup split the workgroup's groups round-robin and
+// are summed through LDS.  Workgroups along gridDim.y split K further; each
+// writes an fp32 partial and the last one to arrive for a column strip (arrival
 // counter) adds the partials in split order and writes bf16.  The counter is
 // reset to zero by that last workgroup, so the workspace needs zeroing once.
 // ---------------------------------------------------------------------------
 template <int MT, int CPL>
-__global__ __launch_bounds__(256) void skinny_kernel(LinearArgs a) {
-  constexpr int WPR = CPL / 4;       // 32-bit words per packed row per lane
+struct SkinnyGroup {
+  static constexpr int WPR = CPL / 4;
+  uint32_t raw[4][4][WPR];  // [K step][packed row][word]
+  bf16x8_t A[MT][4];        // [M subtile][K step]
+  float s[CPL];             // scales of the lane's columns
+};
+
+template <int MT, int CPL, bool FULL>
+__device__ __forceinline__ void skinny_load(const LinearArgs& a, int g, int col0, int mrow0, int lk,
+                                            uint32_t keep0, SkinnyGroup<MT, CPL>& d) {
+  constexpr int WPR = CPL / 4;
+  const bool vec_w = (a.vec & 1) != 0;
+  const bool vec_x = (a.vec & 2) != 0;
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
+#ifdef W4A16_EXP_NOLOAD
+#pragma unroll
+      for (int w = 0; w < WPR; ++w) d.raw[st][r][w] = (uint32_t)(col0 * 2654435761u + pr * 97u + w);
+#else
+      load_packed<CPL, FULL>(a.packed + pr * a.ldp, col0, a.N, vec_w, d.raw[st][r]);
+#endif
+    }
+  // Activations: lane holds x[m][g*128 + 32*st + 8*lk .. +8] for m = 16*mt + l%16.
+  // Rows past M load row M-1 (always valid) and are zeroed by a select, so the
+  // loads carry no per-lane branch.
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mrow0 + 16 * mt;
+    const int mrow = m < a.M ? m : a.M - 1;
+    const uint32_t keep = mt == 0 ? keep0 : (m < a.M ? 0xffffffffu : 0u);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      u32x4_t v = __builtin_bit_cast(
+          u32x4_t, load_x8(a.x + (int64_t)mrow * a.ldx + (int64_t)g * kGroup + st * 32 + lk * 8, vec_x));
+      d.A[mt][st] = as_bf16x8(v & keep);
+    }
+  }
+  load_scales<CPL, FULL>(a.scale + (int64_t)g * a.lds, col0, a.N, vec_w, d.s);
+  (void)WPR;
+}
+
+template <int MT, int CPL>
+__device__ __forceinline__ void skinny_compute(const SkinnyGroup<MT, CPL>& d, f32x4_t (&total)[MT][CPL]) {
+  constexpr int WPR = CPL / 4;
+#ifdef W4A16_EXP_LOADONLY
+  uint32_t h = 0;
+  for (int st = 0; st < 4; ++st) for (int r = 0; r < 4; ++r) for (int w = 0; w < WPR; ++w) h ^= d.raw[st][r][w];
+  total[0][0][0] += __uint_as_float(h & 0x3fffffu) + (float)d.A[0][0][0] + d.s[0];
+  return;
+#endif
+  const bf16x8_t neg136 = as_bf16x8(u32x4_t{kBf16Neg136, kBf16Neg136, kBf16Neg136, kBf16Neg136});
+  // Offset correction -136 * sum_{k in group} x[m, k], in MFMA output layout.
+  f32x4_t cinit[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) c = mfma16(d.A[mt][st], neg136, c);
+    cinit[mt] = c;
+  }
+  // Step-outer: the CPL column accumulators of a step are independent MFMAs.
+  f32x4_t acc[MT][CPL];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+#pragma unroll
+    for (int wi = 0; wi < WPR; ++wi) {
+      Prep pw[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pw[r] = prep(d.raw[st][r][wi]);
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) {
+        const int t = wi * 4 + c4;
+        const bf16x8_t B = as_bf16x8(u32x4_t{pair_dyn(pw[0], c4), pair_dyn(pw[1], c4),
+                                             pair_dyn(pw[2], c4), pair_dyn(pw[3], c4)});
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][t] = mfma16(d.A[mt][st], B, st == 0 ? cinit[mt] : acc[mt][t]);
+      }
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < CPL; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) total[mt][t][r] = __builtin_fmaf(acc[mt][t][r], d.s[t], total[mt][t][r]);
+}
+
+template <int MT, int CPL, int WAVES, bool FULL, bool PIPE>
+__global__ __launch_bounds__(WAVES * 64) void skinny_kernel(LinearArgs a) {
   constexpr int WCOLS = 16 * CPL;    // columns per wave / workgroup
-  extern __shared__ float red[];     // [4 waves][R rows][WCOLS]
+  constexpr int NT = WAVES * 64;
+  extern __shared__ float red[];     // [WAVES][R rows][WCOLS]
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -204,87 +434,45 @@ __global__ __launch_bounds__(256) void skinny_kernel(LinearArgs a) {
   const int G = a.K / kGroup;
   const int g_begin = blockIdx.y * a.gps;
   const int g_end = min(G, g_begin + a.gps);
-  const bool vec_w = (a.vec & 1) != 0;
-  const bool vec_x = (a.vec & 2) != 0;
   const int M = a.M;
   const int N = a.N;
+  const uint32_t keep0 = lc < M ? 0xffffffffu : 0u;
 
+  W4A16_MARK(0);
   f32x4_t total[MT][CPL];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int t = 0; t < CPL; ++t) total[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const bf16x8_t neg136 = as_bf16x8(u32x4_t{kBf16Neg136, kBf16Neg136, kBf16Neg136, kBf16Neg136});
-
-  for (int g = g_begin + wave; g < g_end; g += 4) {
-    // Packed weights of this group: 4 K steps x 4 packed rows x CPL bytes.
-    uint32_t raw[4][4][WPR];
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
-        load_packed<CPL>(a.packed + pr * a.ldp, col0, N, vec_w, raw[st][r]);
-      }
-
-    // Activations: lane holds x[m][g*128 + 32*st + 8*lk .. +8] for m = 16*mt + lc.
-    bf16x8_t A[MT][4];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int m = mt * 16 + lc;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        if (m < M) {
-          A[mt][st] = load_x8(a.x + (int64_t)m * a.ldx + (int64_t)g * kGroup + st * 32 + lk * 8, vec_x);
-        } else {
-          A[mt][st] = as_bf16x8(u32x4_t{0u, 0u, 0u, 0u});
-        }
-      }
+  // This wave's groups are g = g_begin + wave, + WAVES, ...  With PIPE the
+  // next group's loads are issued before the current group is computed.
+  int g = g_begin + wave;
+  if (!PIPE) {
+    for (; g < g_end; g += WAVES) {
+      SkinnyGroup<MT, CPL> cur;
+      skinny_load<MT, CPL, FULL>(a, g, col0, lc, lk, keep0, cur);
+      W4A16_MARK(1);
+      skinny_compute<MT, CPL>(cur, total);
     }
-
-    float s[CPL];
-    load_scales<CPL>(a.scale + (int64_t)g * a.lds, col0, N, vec_w, s);
-
-    // Offset correction -136 * sum_{k in group} x[m, k], in MFMA output layout.
-    f32x4_t cinit[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int st = 0; st < 4; ++st) c = mfma16(A[mt][st], neg136, c);
-      cinit[mt] = c;
-    }
-
-#pragma unroll
-    for (int wi = 0; wi < WPR; ++wi) {
-      Prep pw[4][4];
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pw[st][r] = prep(raw[st][r][wi]);
-#pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) {
-        const int t = wi * 4 + c4;
-        bf16x8_t B[4];
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          B[st] = as_bf16x8(u32x4_t{pair_dyn(pw[st][0], c4), pair_dyn(pw[st][1], c4),
-                                    pair_dyn(pw[st][2], c4), pair_dyn(pw[st][3], c4)});
-        }
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          f32x4_t acc = cinit[mt];
-#pragma unroll
-          for (int st = 0; st < 4; ++st) acc = mfma16(A[mt][st], B[st], acc);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) total[mt][t][r] = __builtin_fmaf(acc[r], s[t], total[mt][t][r]);
-        }
-      }
+  } else if (g < g_end) {
+    SkinnyGroup<MT, CPL> cur, nxt;
+    skinny_load<MT, CPL, FULL>(a, g, col0, lc, lk, keep0, cur);
+    while (true) {
+      const int gn = g + WAVES;
+      if (gn < g_end) skinny_load<MT, CPL, FULL>(a, gn, col0, lc, lk, keep0, nxt);
+      skinny_compute<MT, CPL>(cur, total);
+      if (gn >= g_end) break;
+      const int gnn = gn + WAVES;
+      if (gnn < g_end) skinny_load<MT, CPL, FULL>(a, gnn, col0, lc, lk, keep0, cur);
+      skinny_compute<MT, CPL>(nxt, total);
+      if (gnn >= g_end) break;
+      g = gnn;
     }
   }
 
-  // ---- reduce the 4 waves through LDS (rows < M only) ----
+  W4A16_MARK(3);
+  // ---- reduce the waves through LDS (rows < M only) ----
   const int R = min(M, 16 * MT);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -300,56 +488,159 @@ __global__ __launch_bounds__(256) void skinny_kernel(LinearArgs a) {
       }
     }
   __syncthreads();
+  W4A16_MARK(4);
 
   const int elems = R * WCOLS;
+  auto wave_sum = [&](int e) {
+    float v = red[e];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) v += red[(size_t)w * elems + e];
+    return v;
+  };
   if (a.nsplit == 1) {
-    for (int e = threadIdx.x; e < elems; e += 256) {
+    for (int e = threadIdx.x; e < elems; e += NT) {
       const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
-      if (n < N) {
-        float v = red[e];
-        v += red[(size_t)1 * elems + e];
-        v += red[(size_t)2 * elems + e];
-        v += red[(size_t)3 * elems + e];
-        a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(v);
-      }
+      if (n < N) a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(wave_sum(e));
     }
+    W4A16_MARK(5);
     return;
   }
 
-  // ---- split-K: publish this split's partial, last arrival finishes the strip ----
-  float* part = a.part + (size_t)blockIdx.y * M * N;
-  for (int e = threadIdx.x; e < elems; e += 256) {
-    const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
-    if (n < N) {
-      float v = red[e];
-      v += red[(size_t)1 * elems + e];
-      v += red[(size_t)2 * elems + e];
-      v += red[(size_t)3 * elems + e];
-      part[(size_t)m * N + n] = v;
+  splitk_finish<NT>(a, strip, n0, WCOLS, R, wave_sum);
+  W4A16_MARK(6);
+}
+
+// ---------------------------------------------------------------------------
+// Decode GEMV kernel (M <= 16): the HBM-bound path of batch-1 decode.
+//
+// Workgroup = 4 waves on one strip of 16*CPL columns; blockIdx.y selects a
+// range of gps groups (normally 4, one per wave).  Sized so that every
+// workgroup of a launch is resident at once: the lean register budget
+// (one group in flight per wave, 32-bit row offsets) allows 3+ workgroups per
+// CU, and launches are planned as whole multiples of the CU count where the
+// shape allows.  Order of work in a wave: issue the group's 16 weight loads
+// and its scales, copy the workgroup's activations x[0:M, krange] into LDS,
+// barrier, then unpack + MFMA with A fragments read from LDS.
+// Lane mapping and arithmetic are those of skinny_kernel.
+// ---------------------------------------------------------------------------
+template <int CPL, bool FULL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void gemv_kernel(LinearArgs a) {
+  constexpr int WPR = CPL / 4;
+  constexpr int WCOLS = 16 * CPL;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int lc = lane & 15;
+  const int lk = lane >> 4;
+  const int strip = blockIdx.x;
+  const int n0 = strip * WCOLS;
+  const int col0 = n0 + lc * CPL;
+  const int G = a.K / kGroup;
+  const int g_begin = blockIdx.y * a.gps;
+  const int g_end = min(G, g_begin + a.gps);
+  const int M = a.M, N = a.N;
+  const int kspan = (g_end - g_begin) * kGroup;
+  const int kpitch = a.gps * kGroup + 8;   // +16 B per row against LDS bank conflicts
+  const bool vec_w = (a.vec & 1) != 0;
+  W4A16_MARK(0);
+
+  // Weight loads for this wave's group.  FULL launches use buffer loads: the
+  // per-lane offset (column, k-block row) is fixed and the row of each load
+  // is a scalar offset, so no per-load address arithmetic is needed.
+  int g = g_begin + wave;
+  DecodeSlot<CPL> cur;
+  const uint32_t ldp = (uint32_t)a.ldp;
+  // (Only FULL launches use these; the resources are harmless otherwise.)
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.packed, (uint32_t)((size_t)(a.K / 2) * a.ldp));
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.scale, (uint32_t)((size_t)G * a.lds * 4));
+  const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
+  const uint32_t svoff = (uint32_t)col0 * 4u;
+  auto load_group = [&](int gg) {
+    if constexpr (FULL) {
+      const uint32_t gbase = (uint32_t)gg * kPackedRowsPerGroup * ldp;
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          buffer_load_packed<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, cur.raw[st][r]);
+      const uint32_t soff = (uint32_t)gg * (uint32_t)a.lds * 4u;
+#pragma unroll
+      for (int t = 0; t < CPL; t += 4) {
+        const f32x4_t v = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, svoff + 4u * t, soff, 0));
+        cur.s[t] = v[0]; cur.s[t + 1] = v[1]; cur.s[t + 2] = v[2]; cur.s[t + 3] = v[3];
+      }
+    } else {
+      const uint8_t* base = a.packed + (int64_t)gg * kPackedRowsPerGroup * a.ldp;
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t off = (uint32_t)((st * 16 + lk * 4 + r) * ldp);
+          load_packed<CPL, FULL>(base + off, col0, N, vec_w, cur.raw[st][r]);
+        }
+      load_scales<CPL, FULL>(a.scale + (int64_t)gg * a.lds, col0, N, vec_w, cur.s);
+    }
+  };
+  if (g < g_end) load_group(g);
+  W4A16_MARK(1);
+
+  // Activations of the workgroup's K range -> LDS.
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+  {
+    const bool vec_x = (a.vec & 2) != 0;
+    const int chunks = kspan / 8;
+    for (int i = threadIdx.x; i < M * chunks; i += 256) {
+      const int m = i / chunks, c = i % chunks;
+      const uint16_t* src = a.x + (int64_t)m * a.ldx + (int64_t)g_begin * kGroup + c * 8;
+      *reinterpret_cast<u32x4_t*>(xs + m * kpitch + c * 8) = __builtin_bit_cast(u32x4_t, load_x8(src, vec_x));
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
-  __shared__ int is_last;
-  if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(a.counters + strip, 1u, __ATOMIC_ACQ_REL,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (prev == (uint32_t)(a.nsplit - 1));
+  W4A16_MARK(2);
+
+  const uint32_t keep = lc < M ? 0xffffffffu : 0u;
+  const int xrow_idx = lc < M ? lc : M - 1;
+  f32x4_t total[CPL];
+#pragma unroll
+  for (int t = 0; t < CPL; ++t) total[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  while (g < g_end) {
+    decode_compute<CPL>(cur, xs, kpitch, g - g_begin, xrow_idx, lk, keep, total);
+    g += 4;
+    if (g < g_end) load_group(g);
   }
+  W4A16_MARK(3);
+
+  // Reduce the 4 waves through LDS (reusing the activation buffer).
   __syncthreads();
-  if (!is_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  for (int e = threadIdx.x; e < elems; e += 256) {
-    const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
-    if (n < N) {
-      float v = 0.f;
-      for (int sp = 0; sp < a.nsplit; ++sp)
-        v += __builtin_nontemporal_load(a.part + ((size_t)sp * M + m) * N + n);
-      a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(v);
+  float* red = smem;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = lk * 4 + r;
+    if (m < M) {
+      float* dst = red + ((size_t)wave * M + m) * WCOLS + lc * CPL;
+#pragma unroll
+      for (int t = 0; t < CPL; t += 4)
+        *reinterpret_cast<f32x4_t*>(dst + t) = f32x4_t{total[t][r], total[t + 1][r], total[t + 2][r], total[t + 3][r]};
     }
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(a.counters + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  W4A16_MARK(4);
+  const int elems = M * WCOLS;
+  auto wave_sum = [&](int e) {
+    return ((red[e] + red[(size_t)elems + e]) + red[(size_t)2 * elems + e]) + red[(size_t)3 * elems + e];
+  };
+  if (a.nsplit == 1) {
+    for (int e = threadIdx.x; e < elems; e += 256) {
+      const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
+      if (n < N) a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(wave_sum(e));
+    }
+    W4A16_MARK(5);
+    return;
+  }
+  splitk_finish<256>(a, strip, n0, WCOLS, M, wave_sum);
+  W4A16_MARK(6);
+  (void)WPR;
 }
 
 // ---------------------------------------------------------------------------
@@ -399,6 +690,7 @@ constexpr int kGemmCols = 256;
 constexpr int kGemmMT = 8;      // 16-row subtiles per wave
 constexpr int kGemmBand = 4;    // row tiles per column band
 
+template <bool FULL>
 __global__ __launch_bounds__(256) void gemm_kernel(LinearArgs a) {
   __shared__ u32x4_t As[2][4 * kGemmMT * 64];  // [buf][step][subtile][lane] 16 B each
   __shared__ __attribute__((aligned(16))) float Cs[2][kGemmRows];
@@ -457,7 +749,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(LinearArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
         uint32_t w[1];
-        load_packed<4>(a.packed + pr * a.ldp, col0, N, vec_w, w);
+        load_packed<4, FULL>(a.packed + pr * a.ldp, col0, N, vec_w, w);
         raw[st][r] = w[0];
       }
   };
@@ -475,7 +767,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(LinearArgs a) {
     stage_a_load(0, abuf);
     const float cv = stage_c_load(0);
     load_b(0, raw);
-    load_scales<4>(a.scale, col0, N, vec_w, s);
+    load_scales<4, FULL>(a.scale, col0, N, vec_w, s);
     stage_a_store(0, abuf);
     if (threadIdx.x < kGemmRows) Cs[0][threadIdx.x] = cv;
   }
@@ -494,7 +786,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(LinearArgs a) {
       stage_a_load(g + 1, abuf);
       cv_n = stage_c_load(g + 1);
       load_b(g + 1, raw_n);
-      load_scales<4>(a.scale + (int64_t)(g + 1) * a.lds, col0, N, vec_w, s_n);
+      load_scales<4, FULL>(a.scale + (int64_t)(g + 1) * a.lds, col0, N, vec_w, s_n);
     }
 
     // Unpack this wave's weights for the whole group: B[step][column].
@@ -607,8 +899,9 @@ __global__ __launch_bounds__(256) void zero_kernel(uint16_t* __restrict__ y, int
 // Host-side planning.
 // ---------------------------------------------------------------------------
 struct Plan {
-  int kind;    // 0 = skinny, 1 = gemm
-  int mt, cpl; // skinny variant
+  int kind;    // 0 = skinny, 1 = gemm, 2 = gemv (M <= 16, activations in LDS)
+  size_t lds_bytes;
+  int mt, cpl, waves, pipe;  // skinny variant
   int strips, nsplit, gps;
   size_t ws_bytes;
 };
@@ -616,6 +909,15 @@ struct Plan {
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int env_int(const char* name, int dflt) {
+#ifdef W4A16_EXP
+  const char* v = getenv(name);
+  if (v) return atoi(v);
+#endif
+  (void)name;
+  return dflt;
+}
 
 Plan make_plan(int M, int N, int K) {
   Plan p{};
@@ -625,19 +927,41 @@ Plan make_plan(int M, int N, int K) {
     p.ws_bytes = (size_t)kCounterBytes + (size_t)G * M * sizeof(float);
     return p;
   }
+  // GEMV kernel: 4 waves x one 128-row group each per workgroup; activations
+  // of the workgroup's K range staged in LDS.
+  if (M <= 16 && G > 0 && env_int("W4A16_GEMV", 1)) {
+    p.kind = 2;
+    p.cpl = env_int("W4A16_CPL", 8);
+    p.strips = ceil_div(N, 16 * p.cpl);
+    p.gps = env_int("W4A16_GPS", 4);
+    p.nsplit = ceil_div(G, p.gps);
+    p.lds_bytes = (size_t)M * (p.gps * kGroup + 8) * 2;
+    const size_t rbytes = (size_t)4 * M * 16 * p.cpl * 4;
+    if (rbytes > p.lds_bytes) p.lds_bytes = rbytes;
+    p.ws_bytes = p.nsplit > 1 ? (size_t)kCounterBytes + (size_t)p.nsplit * M * N * sizeof(float) : 0;
+    return p;
+  }
   p.kind = 0;
   p.mt = M <= 16 ? 1 : 2;
-  p.cpl = (p.mt == 1 && N >= 4096) ? 16 : 8;
+  p.cpl = env_int("W4A16_CPL", 8);
+  if (p.mt == 2 && p.cpl == 16) p.cpl = 8;
+  const int R = M < 16 * p.mt ? M : 16 * p.mt;
+  // Waves per workgroup: as many as the LDS reduction buffer allows (<= 64 KB).
+  int waves = 16;
+  while (waves > 4 && (size_t)waves * R * 16 * p.cpl * 4 > 65536) waves >>= 1;
+  p.waves = env_int("W4A16_WAVES", waves);
+  p.pipe = env_int("W4A16_PIPE", 0);
   p.strips = ceil_div(N, 16 * p.cpl);
-  // Enough workgroups to keep every CU streaming (~2 per CU), bounded so the
-  // fp32 partial traffic (write + read) stays within a quarter of the weight bytes.
-  const int want = ceil_div(512, p.strips);
+  // Split K across workgroups until ~16 waves per CU are resident, keeping at
+  // least one group per wave and the fp32 partial traffic (write + read) within
+  // a quarter of the weight bytes.
+  int nsplit = ceil_div(256 * 16, (int64_t)p.strips * p.waves);
   const int by_traffic = (int)((int64_t)K / (64 * (int64_t)M));
-  int nsplit = want;
   if (nsplit > by_traffic) nsplit = by_traffic;
-  const int max_split = ceil_div(G, 4);  // at least one group per wave
+  const int max_split = ceil_div(G, p.waves);
   if (nsplit > max_split) nsplit = max_split;
   if (nsplit < 1) nsplit = 1;
+  nsplit = env_int("W4A16_NSPLIT", nsplit);
   p.gps = G > 0 ? ceil_div(G, nsplit) : 0;
   p.nsplit = G > 0 ? ceil_div(G, p.gps) : 1;
   p.ws_bytes = p.nsplit > 1 ? (size_t)kCounterBytes + (size_t)p.nsplit * M * N * sizeof(float) : 0;
@@ -649,12 +973,51 @@ int launch_status() {
   return e == hipSuccess ? W4A16_OK : W4A16_ERR_LAUNCH;
 }
 
+template <int CPL>
+int launch_gemv_c(const LinearArgs& a, const Plan& p, hipStream_t stream) {
+  // Buffer loads address at most 4 GiB per resource.
+  const bool full = (a.vec & 1) && (a.N % (16 * CPL) == 0) && (size_t)(a.K / 2) * a.ldp < 0xffffffffull &&
+                    (size_t)(a.K / kGroup) * a.lds * 4 < 0xffffffffull;
+  if (full)
+    hipLaunchKernelGGL((gemv_kernel<CPL, true>), dim3(p.strips, p.nsplit), dim3(256), p.lds_bytes, stream, a);
+  else
+    hipLaunchKernelGGL((gemv_kernel<CPL, false>), dim3(p.strips, p.nsplit), dim3(256), p.lds_bytes, stream, a);
+  return launch_status();
+}
+
+int launch_gemv(const LinearArgs& a, const Plan& p, hipStream_t stream) {
+  if (p.cpl == 4) return launch_gemv_c<4>(a, p, stream);
+  if (p.cpl == 16) return launch_gemv_c<16>(a, p, stream);
+  return launch_gemv_c<8>(a, p, stream);
+}
+
+template <int MT, int CPL, int WAVES, bool PIPE>
+int launch_skinny_p(const LinearArgs& a, const Plan& p, hipStream_t stream) {
+  const int R = a.M < 16 * MT ? a.M : 16 * MT;
+  const size_t shmem = (size_t)WAVES * R * 16 * CPL * sizeof(float);
+  const bool full = (a.vec & 1) && (a.N % (16 * CPL) == 0);
+  if (full)
+    hipLaunchKernelGGL((skinny_kernel<MT, CPL, WAVES, true, PIPE>), dim3(p.strips, p.nsplit), dim3(WAVES * 64),
+                       shmem, stream, a);
+  else
+    hipLaunchKernelGGL((skinny_kernel<MT, CPL, WAVES, false, PIPE>), dim3(p.strips, p.nsplit), dim3(WAVES * 64),
+                       shmem, stream, a);
+  return launch_status();
+}
+
+template <int MT, int CPL, int WAVES>
+int launch_skinny_w(const LinearArgs& a, const Plan& p, hipStream_t stream) {
+  if (p.pipe) return launch_skinny_p<MT, CPL, WAVES, true>(a, p, stream);
+  return launch_skinny_p<MT, CPL, WAVES, false>(a, p, stream);
+}
+
 template <int MT, int CPL>
 int launch_skinny(const LinearArgs& a, const Plan& p, hipStream_t stream) {
-  const int R = a.M < 16 * MT ? a.M : 16 * MT;
-  const size_t shmem = (size_t)4 * R * 16 * CPL * sizeof(float);
-  hipLaunchKernelGGL((skinny_kernel<MT, CPL>), dim3(p.strips, p.nsplit), dim3(256), shmem, stream, a);
-  return launch_status();
+  switch (p.waves) {
+    case 16: return launch_skinny_w<MT, CPL, 16>(a, p, stream);
+    case 8: return launch_skinny_w<MT, CPL, 8>(a, p, stream);
+    default: return launch_skinny_w<MT, CPL, 4>(a, p, stream);
+  }
 }
 
 }  // namespace
@@ -706,7 +1069,7 @@ int w4a16_linear(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, 
 
   const Plan p = make_plan(M, N, K);
   if (p.ws_bytes > 0 && (!workspace || workspace_bytes < p.ws_bytes)) return W4A16_ERR_WORKSPACE;
-  if (p.kind == 0 && p.nsplit > 1 && p.strips > kMaxStrips) return W4A16_ERR_TOO_LARGE;
+  if (p.kind != 1 && p.nsplit > 1 && p.strips > kMaxStrips) return W4A16_ERR_TOO_LARGE;
 
   LinearArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -724,6 +1087,9 @@ int w4a16_linear(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, 
   const bool vx = aligned16(x) && (ldx % 8 == 0);
   const bool vy = (((uintptr_t)y & 7u) == 0) && (ldy % 4 == 0);
   a.vec = (vw ? 1 : 0) | (vx ? 2 : 0) | (vy ? 4 : 0);
+#ifdef W4A16_EXP
+  a.trace = getenv("W4A16_TRACE") ? reinterpret_cast<uint64_t*>(strtoull(getenv("W4A16_TRACE"), nullptr, 0)) : nullptr;
+#endif
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (K == 0) {
@@ -753,7 +1119,10 @@ int w4a16_linear(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, 
     if (rc != W4A16_OK) return rc;
     int blocks = a.mtiles * a.ntiles;
     blocks = (blocks + 7) & ~7;
-    hipLaunchKernelGGL(gemm_kernel, dim3(blocks), dim3(256), 0, s, a);
+    if ((a.vec & 1) && N % kGemmCols == 0)
+      hipLaunchKernelGGL(gemm_kernel<true>, dim3(blocks), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(gemm_kernel<false>, dim3(blocks), dim3(256), 0, s, a);
     return launch_status();
   }
 
@@ -763,8 +1132,11 @@ int w4a16_linear(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, 
     a.counters = static_cast<uint32_t*>(workspace);
     a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
   }
+  if (p.kind == 2) return launch_gemv(a, p, s);
   if (p.mt == 1 && p.cpl == 16) return launch_skinny<1, 16>(a, p, s);
+  if (p.mt == 1 && p.cpl == 4) return launch_skinny<1, 4>(a, p, s);
   if (p.mt == 1) return launch_skinny<1, 8>(a, p, s);
+  if (p.cpl == 4) return launch_skinny<2, 4>(a, p, s);
   return launch_skinny<2, 8>(a, p, s);
 }
 
