@@ -28,6 +28,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "../../include/w4a16.h"
 
 namespace {
@@ -675,12 +677,17 @@ __global__ __launch_bounds__(256) void rowsum_kernel(const uint16_t* __restrict_
 // GEMM kernel (M > 32).
 //
 // Workgroup tile 128 rows x 256 columns, 4 waves side by side along N, each
-// wave 128 x 64.  Per 128-row K group the workgroup stages the activation tile
-// (128 x 128 bf16, 32 KB) in LDS in MFMA fragment order, double buffered, and
-// each wave keeps its own packed weights in registers (4 columns per lane, 16
-// loads of 4 bytes per group), unpacks them once into 16 bf16 B fragments and
-// applies them to the 8 M-subtiles:
-//   acc = -rowsum*136 ; acc += x . (q + 136) over 4 K steps ; total += acc * scale.
+// wave 128 x 64 (8 M-subtiles x 4 MFMA column blocks, 4 columns per lane).
+// Per 128-row K group:
+//  * the activation tile (128 x 128 bf16, 32 KB) is copied global -> LDS with
+//    direct-to-LDS loads in MFMA fragment order (wave w copies K step w),
+//    double buffered, together with the group's 128 row sums (rowsum_kernel);
+//  * each wave loads its own packed weights (16 buffer loads of 4 bytes,
+//    scalar row offsets) and scales one group ahead, in registers;
+//  * running-ratio fold: the accumulator U is kept in units of the current
+//    group's scale, U <- U * (s_prev / s) - 136 * rowsum, so one fp32
+//    accumulator set suffices and the MFMAs accumulate straight into it;
+//    the output is U * s_last (see clamp_scale for zero / tiny scales).
 // Tiles are handed out XCD-major: workgroup b runs on XCD b % 8, and each XCD
 // receives a contiguous range of tile ids, ordered in column bands of 4 row
 // tiles, so the rows of x and the weight columns an XCD touches stay in its L2.
@@ -690,13 +697,25 @@ constexpr int kGemmCols = 256;
 constexpr int kGemmMT = 8;      // 16-row subtiles per wave
 constexpr int kGemmBand = 4;    // row tiles per column band
 
+// Scale magnitudes below 1e-20 (zero, subnormal or tiny) are raised to 1e-20
+// in the GEMM fold so that the running ratio stays finite; such a group then
+// contributes at most 1e-20 * sum|x*q| instead of exactly 0.  Non-finite
+// scales pass through and make the column non-finite, as in the reference.
+__device__ __forceinline__ float clamp_scale(float s) {
+  const float a = __builtin_fabsf(s);
+  return a < 1e-20f ? __builtin_copysignf(1e-20f, s) : s;
+}
+
 template <bool FULL>
-__global__ __launch_bounds__(256) void gemm_kernel(LinearArgs a) {
+#ifndef W4A16_GEMM_WAVES
+#define W4A16_GEMM_WAVES 2
+#endif
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W4A16_GEMM_WAVES, 8))) void gemm_kernel(LinearArgs a) {
   __shared__ u32x4_t As[2][4 * kGemmMT * 64];  // [buf][step][subtile][lane] 16 B each
   __shared__ __attribute__((aligned(16))) float Cs[2][kGemmRows];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lc = lane & 15;
   const int lk = lane >> 4;
   const int M = a.M, N = a.N;
@@ -717,111 +736,128 @@ __global__ __launch_bounds__(256) void gemm_kernel(LinearArgs a) {
   const int in_band = tid_lin % band_size;
   const int m_tile = first_m + in_band % band_rows;
   const int n_tile = in_band / band_rows;
-
   const int m0 = m_tile * kGemmRows;
   const int col0 = n_tile * kGemmCols + wave * 64 + lc * 4;
   const bool vec_w = (a.vec & 1) != 0;
 
-  // ---- staging helpers ----
-  // Wave w stages K step w: 8 subtiles x 64 lanes x 16 B.  Lane l of subtile i
-  // loads row m0 + 16*i + l%16, columns 8*(4*w + l/16) .. +8 of the group.
-  auto stage_a_load = [&](int g, u32x4_t (&buf)[kGemmMT]) {
+  // ---- operand sources ----
+  const uint32_t ldp = (uint32_t)a.ldp;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.packed, (uint32_t)((size_t)(a.K / 2) * a.ldp));
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.scale, (uint32_t)((size_t)G * a.lds * 4));
+  const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
+  // Activation rows this lane copies (clamped: rows past M compute values that are never stored).
+  const uint16_t* xlane = a.x + (int64_t)(m0 + lc) * a.ldx + (wave * 4 + lk) * 8;
+  const int64_t xstep = (int64_t)16 * a.ldx;     // 16 rows
+  const int last_full = (M - 1 - m0 - lc) / 16;  // subtiles whose row m0 + 16i + lc < M
+  int crow = m0 + (threadIdx.x & 127);
+  crow = crow < M ? crow : M - 1;
+
+  auto stage_a = [&](int g, int b) {
 #pragma unroll
     for (int i = 0; i < kGemmMT; ++i) {
-      int row = m0 + 16 * i + lc;
-      row = row < M ? row : M - 1;  // rows past M compute garbage that is never stored
-      const uint16_t* p = a.x + (int64_t)row * a.ldx + (int64_t)g * kGroup + (wave * 4 + lk) * 8;
-      buf[i] = *reinterpret_cast<const u32x4_t*>(p);
+      const int ii = i <= last_full ? i : last_full;
+      const uint16_t* src = xlane + (int64_t)ii * xstep + (int64_t)g * kGroup;
+      __builtin_amdgcn_global_load_lds((const void*)src,
+                                       (void __attribute__((address_space(3)))*)&As[b][(wave * kGemmMT + i) * 64],
+                                       16, 0, 0);
+    }
+    if (wave < 2)
+      __builtin_amdgcn_global_load_lds((const void*)(a.part + (int64_t)g * M + crow),
+                                       (void __attribute__((address_space(3)))*)&Cs[b][wave * 64], 4, 0, 0);
+  };
+  auto load_b = [&](int g, uint32_t (&raw)[4][4], float (&s)[4]) {
+    if constexpr (FULL) {
+      const uint32_t gbase = (uint32_t)g * kPackedRowsPerGroup * ldp;
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          raw[st][r] = __builtin_amdgcn_raw_buffer_load_b32(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, 0);
+      const f32x4_t v = __builtin_bit_cast(
+          f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, (uint32_t)col0 * 4u, (uint32_t)g * (uint32_t)a.lds * 4u, 0));
+      s[0] = v[0]; s[1] = v[1]; s[2] = v[2]; s[3] = v[3];
+    } else {
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
+          uint32_t w[1];
+          load_packed<4, false>(a.packed + pr * a.ldp, col0, N, vec_w, w);
+          raw[st][r] = w[0];
+        }
+      load_scales<4, false>(a.scale + (int64_t)g * a.lds, col0, N, vec_w, s);
     }
   };
-  auto stage_a_store = [&](int b, const u32x4_t (&buf)[kGemmMT]) {
-#pragma unroll
-    for (int i = 0; i < kGemmMT; ++i) As[b][(wave * kGemmMT + i) * 64 + lane] = buf[i];
-  };
-  auto stage_c_load = [&](int g) -> float {
-    const int row = m0 + threadIdx.x;
-    return (threadIdx.x < kGemmRows && row < M) ? a.part[(int64_t)g * M + row] : 0.f;
-  };
-  auto load_b = [&](int g, uint32_t (&raw)[4][4]) {
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
-        uint32_t w[1];
-        load_packed<4, FULL>(a.packed + pr * a.ldp, col0, N, vec_w, w);
-        raw[st][r] = w[0];
-      }
-  };
 
-  f32x4_t total[kGemmMT][4];
+  f32x4_t U[kGemmMT][4];
 #pragma unroll
   for (int i = 0; i < kGemmMT; ++i)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) total[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < 4; ++t) U[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   uint32_t raw[4][4];
   float s[4];
-  {
-    u32x4_t abuf[kGemmMT];
-    stage_a_load(0, abuf);
-    const float cv = stage_c_load(0);
-    load_b(0, raw);
-    load_scales<4, FULL>(a.scale, col0, N, vec_w, s);
-    stage_a_store(0, abuf);
-    if (threadIdx.x < kGemmRows) Cs[0][threadIdx.x] = cv;
-  }
+  float s_ref[4];      // scale U is currently expressed in (per column)
+  load_b(0, raw, s);
+  stage_a(0, 0);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) s_ref[t] = clamp_scale(s[t]);
 
   for (int g = 0; g < G; ++g) {
     const int b = g & 1;
+    // Direct-to-LDS copies of this group (issued one iteration earlier) must
+    // have landed before the barrier publishes them.
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     __syncthreads();
 
-    // Prefetch the next group while this one computes.
     const bool has_next = g + 1 < G;
-    u32x4_t abuf[kGemmMT];
     uint32_t raw_n[4][4];
     float s_n[4];
-    float cv_n = 0.f;
     if (has_next) {
-      stage_a_load(g + 1, abuf);
-      cv_n = stage_c_load(g + 1);
-      load_b(g + 1, raw_n);
-      load_scales<4, FULL>(a.scale + (int64_t)(g + 1) * a.lds, col0, N, vec_w, s_n);
+      stage_a(g + 1, b ^ 1);
+      load_b(g + 1, raw_n, s_n);
     }
 
-    // Unpack this wave's weights for the whole group: B[step][column].
-    bf16x8_t B[4][4];
+    // Fold: U <- U * (s_ref / s) - 136 * rowsum.  (U is zero before the first
+    // group, where the ratio is 1.)  s_ref / s uses the hardware reciprocal:
+    // relative error ~1 ulp, the order of the fp32 rounding of the fold.
+    float rho[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float sc = clamp_scale(s[t]);
+      rho[t] = s_ref[t] * __builtin_amdgcn_rcpf(sc);
+      s_ref[t] = sc;
+    }
+#pragma unroll
+    for (int i = 0; i < kGemmMT; ++i) {
+      const f32x4_t c4 = *reinterpret_cast<const f32x4_t*>(&Cs[b][16 * i + 4 * lk]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) U[i][t][r] = __builtin_fmaf(U[i][t][r], rho[t], -c4[r]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       Prep p[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) p[r] = prep(raw[st][r]);
-      B[st][0] = as_bf16x8(u32x4_t{pair_of<0>(p[0]), pair_of<0>(p[1]), pair_of<0>(p[2]), pair_of<0>(p[3])});
-      B[st][1] = as_bf16x8(u32x4_t{pair_of<1>(p[0]), pair_of<1>(p[1]), pair_of<1>(p[2]), pair_of<1>(p[3])});
-      B[st][2] = as_bf16x8(u32x4_t{pair_of<2>(p[0]), pair_of<2>(p[1]), pair_of<2>(p[2]), pair_of<2>(p[3])});
-      B[st][3] = as_bf16x8(u32x4_t{pair_of<3>(p[0]), pair_of<3>(p[1]), pair_of<3>(p[2]), pair_of<3>(p[3])});
-    }
-
+      bf16x8_t B[4];
+      B[0] = as_bf16x8(u32x4_t{pair_of<0>(p[0]), pair_of<0>(p[1]), pair_of<0>(p[2]), pair_of<0>(p[3])});
+      B[1] = as_bf16x8(u32x4_t{pair_of<1>(p[0]), pair_of<1>(p[1]), pair_of<1>(p[2]), pair_of<1>(p[3])});
+      B[2] = as_bf16x8(u32x4_t{pair_of<2>(p[0]), pair_of<2>(p[1]), pair_of<2>(p[2]), pair_of<2>(p[3])});
+      B[3] = as_bf16x8(u32x4_t{pair_of<3>(p[0]), pair_of<3>(p[1]), pair_of<3>(p[2]), pair_of<3>(p[3])});
 #pragma unroll
-    for (int i = 0; i < kGemmMT; ++i) {
-      bf16x8_t A[4];
+      for (int i = 0; i < kGemmMT; ++i) {
+        const bf16x8_t A = __builtin_bit_cast(bf16x8_t, As[b][(st * kGemmMT + i) * 64 + lane]);
 #pragma unroll
-      for (int st = 0; st < 4; ++st) A[st] = __builtin_bit_cast(bf16x8_t, As[b][(st * kGemmMT + i) * 64 + lane]);
-      const f32x4_t c4 = *reinterpret_cast<const f32x4_t*>(&Cs[b][16 * i + 4 * lk]);
-      const f32x4_t cinit = -c4;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        f32x4_t acc = cinit;
-#pragma unroll
-        for (int st = 0; st < 4; ++st) acc = mfma16(A[st], B[st][t], acc);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) total[i][t][r] = __builtin_fmaf(acc[r], s[t], total[i][t][r]);
+        for (int t = 0; t < 4; ++t) U[i][t] = mfma16(A, B[t], U[i][t]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
 
     if (has_next) {
-      stage_a_store(b ^ 1, abuf);
-      if (threadIdx.x < kGemmRows) Cs[b ^ 1][threadIdx.x] = cv_n;
 #pragma unroll
       for (int st = 0; st < 4; ++st)
 #pragma unroll
@@ -831,8 +867,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(LinearArgs a) {
     }
   }
 
-  // ---- store: lane holds rows m0 + 16i + 4lk + r, columns col0 .. col0+3 ----
-  const bool vec_y = (a.vec & 4) != 0 && col0 + 4 <= N;
+  // ---- store y = U * s_ref: lane holds rows m0 + 16i + 4lk + r, columns col0 .. col0+3 ----
+  const float* outs = s_ref;
+  const bool vec_y = FULL ? (a.vec & 4) != 0 : ((a.vec & 4) != 0 && col0 + 4 <= N);
 #pragma unroll
   for (int i = 0; i < kGemmMT; ++i)
 #pragma unroll
@@ -840,10 +877,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(LinearArgs a) {
       const int m = m0 + 16 * i + 4 * lk + r;
       if (m >= M) continue;
       uint16_t* dst = a.y + (int64_t)m * a.ldy + col0;
-      const uint16_t h0 = f32_to_bf16(total[i][0][r]);
-      const uint16_t h1 = f32_to_bf16(total[i][1][r]);
-      const uint16_t h2 = f32_to_bf16(total[i][2][r]);
-      const uint16_t h3 = f32_to_bf16(total[i][3][r]);
+      const uint16_t h0 = f32_to_bf16(U[i][0][r] * outs[0]);
+      const uint16_t h1 = f32_to_bf16(U[i][1][r] * outs[1]);
+      const uint16_t h2 = f32_to_bf16(U[i][2][r] * outs[2]);
+      const uint16_t h3 = f32_to_bf16(U[i][3][r] * outs[3]);
       if (vec_y) {
         *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{(uint32_t)h0 | ((uint32_t)h1 << 16),
                                                    (uint32_t)h2 | ((uint32_t)h3 << 16)};

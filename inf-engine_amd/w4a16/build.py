@@ -23,6 +23,10 @@ FLAGS = [
     "-shared",
     # Keep the compiler from forming packed-fp32 VALU ops (v_pk_*_f32).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: the kernels rescale their
+    # accumulators with VALU ops every 128-row group, which on AGPRs costs a
+    # read and a write per element.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 
