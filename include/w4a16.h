@@ -25,22 +25,42 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 1
+#define W4A16_ABI_VERSION 2
+
+/* Most problems one grouped call accepts. */
+#define W4A16_MAX_PROBLEMS 8
 
 /* Status codes. */
 #define W4A16_OK 0
 #define W4A16_ERR_NULL 1        /* a required pointer is NULL */
-#define W4A16_ERR_SHAPE 2       /* negative size, or a leading dimension smaller than the row */
+#define W4A16_ERR_SHAPE 2       /* negative size, leading dimension smaller than the row, or bad count */
 #define W4A16_ERR_K_GROUP 3     /* K not a multiple of group_size, or odd */
 #define W4A16_ERR_GROUP_SIZE 4  /* group_size unsupported (linear: must be 128) */
 #define W4A16_ERR_WORKSPACE 5   /* workspace NULL or smaller than w4a16_workspace_size() */
 #define W4A16_ERR_LAUNCH 6      /* a HIP launch reported an error */
 #define W4A16_ERR_DTYPE 7       /* unknown dtype code */
-#define W4A16_ERR_TOO_LARGE 8   /* N exceeds the split-K counter table (4,194,304 columns) */
+#define W4A16_ERR_TOO_LARGE 8   /* more split-K strips / tiles than the 16,384 workspace counters */
 
 /* dtype codes for w4a16_dequant. */
 #define W4A16_DTYPE_F32 0
 #define W4A16_DTYPE_BF16 1
+
+/*
+ * One projection y[M, N] = x[M, K] @ W[K, N] of a grouped call (all problems
+ * of a call share M).  Layouts as for w4a16_linear.
+ */
+typedef struct w4a16_problem {
+  const void* x;        /* bf16 [M, K] */
+  int64_t ldx;
+  const int8_t* packed; /* [K/2, N] */
+  int64_t ldp;
+  const float* scale;   /* [K/128, N] */
+  int64_t lds;
+  void* y;              /* bf16 [M, N] */
+  int64_t ldy;
+  int N;
+  int K;
+} w4a16_problem;
 
 /* Version of this ABI (W4A16_ABI_VERSION of the build). */
 int w4a16_abi_version(void);
@@ -71,7 +91,7 @@ int w4a16_workspace_size(int M, int N, int K, int group_size, size_t* bytes);
  * group_size must be 128 (the reference asserts the same,
  * engine/kernels/quant.py:267).  K must be a multiple of 128.  M == 0 or
  * N == 0 is a no-op; K == 0 writes zeros.  M <= 32 runs the bandwidth-bound
- * skinny kernel, M > 32 the MFMA GEMM.
+ * decode kernels, M > 32 the MFMA GEMM.
  */
 int w4a16_linear(const void* x, int64_t ldx,
                  const int8_t* packed, int64_t ldp,
@@ -80,6 +100,25 @@ int w4a16_linear(const void* x, int64_t ldx,
                  int M, int N, int K, int group_size,
                  void* workspace, size_t workspace_bytes,
                  void* stream);
+
+/*
+ * Several independent projections in one launch: up to W4A16_MAX_PROBLEMS
+ * problems sharing M, each with its own activations, weights and output
+ * (problems may share x, e.g. q/k/v or gate/up of a decoder block).  Same
+ * arithmetic and status codes as w4a16_linear; the workspace must be at least
+ * w4a16_workspace_size_grouped() for the same table.
+ *
+ * No counterpart in the reference, which calls int4_matmul once per projection
+ * (engine/llama_attention.py:83-85, engine/llama_mlp.py:30-33,
+ * engine/llama_moe.py:90-105).  It is the fused-projection path for those call
+ * sites: one launch streams all the listed weights.
+ */
+int w4a16_linear_grouped(const w4a16_problem* problems, int count, int M, int group_size,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes w4a16_linear_grouped needs for this problem table. */
+int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int M, int group_size,
+                                 size_t* bytes);
 
 /*
  * out[K, N] = q[K, N] * scale[k / group_size, n]  in fp32 (out_dtype

@@ -1,80 +1,77 @@
 // W4A16 fused linear for MI355X (gfx950): y[M,N] = x[M,K] (bf16) @ W[K,N],
-// W stored as packed signed INT4 with one fp32 scale per 128-row K group.
+// W stored as packed signed INT4 with one fp32 scale per 128-row K group
+// (format and nibble arithmetic: w4a16_device.h).
 //
-// Weight format (fixed by the reference, engine/kernels/quant.py:115-118,141-146):
-//   packed[k/2, n] int8: bits 7..4 = q[2i, n] (even K row), bits 3..0 = q[2i+1, n]
-//   (odd K row), both 4-bit two's complement in [-8, 7];
-//   scale[k/128, n] fp32;  W[k, n] = q[k, n] * scale[k/128, n].
-// Contraction order (engine/kernels/quant.py:221-234): per 128-row group the dot
-// product of bf16 activations with the integer weights is formed in fp32, then
-// multiplied by the fp32 scale and added to an fp32 accumulator; the result is
-// rounded once to bf16.
+// Contraction order (engine/kernels/quant.py:221-234): per 128-row group the
+// dot product of bf16 activations with the integer weights is formed in fp32,
+// then multiplied by the fp32 scale and added to an fp32 accumulator; the
+// result is rounded once to bf16.
 //
-// Kernels in this file:
-//   skinny_kernel   M <= 32 (decode, batched decode, speculative verify).  HBM bound.
-//   rowsum_kernel   per-(group,row) activation sums used by gemm_kernel.
-//   gemm_kernel     M > 32 (prefill).  MFMA bound.
-//   dequant_kernel  packed -> dense weights (bit-exactness probe of the unpack).
-//
-// Nibble -> bf16 conversion used by both matrix kernels.  Flipping bit 3 of a
-// two's complement nibble q gives u = q + 8 in [0, 15].  The bf16 bit pattern
-// 0x4300 | u is exactly 128 + u, so one byte permute plus one and-or turns a
-// packed byte into a pair of bf16 values (128 + u_even, 128 + u_odd).  The MFMA
-// therefore produces sum_k x[k] * (q[k] + 136); the 136 * sum_k x[k] offset is
-// removed per (row, group) before the scale is applied, which keeps the
-// per-group partial exact up to fp32 accumulation rounding.
+// A launch processes a table of up to kMaxProblems independent projections
+// that share M (one problem for the drop-in int4_matmul; q/k/v or gate/up or
+// a set of MoE experts for grouped calls).  Kernels:
+//   gemv_kernel     M <= 16  (decode)                       HBM bound
+//   skinny_kernel   16 < M <= 32 (batched decode / verify)  HBM bound, one problem
+//   rowsum_kernel   per-(group,row) activation sums for gemm_kernel
+//   gemm_kernel     M > 32 (prefill)                        MFMA bound
+//   dequant_kernel  packed -> dense weights (bit-exactness probe of the unpack)
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdlib.h>
 
-#include <type_traits>
+#include <algorithm>
 
 #include "../../include/w4a16.h"
+#include "w4a16_device.h"
+
+using namespace w4a16;
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+constexpr int kMaxProblems = W4A16_MAX_PROBLEMS;
+constexpr int kCounterBytes = 65536;           // split-K arrival counters at the head of the workspace
+constexpr int kMaxCounters = kCounterBytes / 4;
 
-constexpr int kGroup = 128;                 // K rows per scale group
-constexpr int kPackedRowsPerGroup = kGroup / 2;
-constexpr uint32_t kBf16Base = 0x43004300u; // bf16 128.0 in both halves
-constexpr uint32_t kBf16Neg136 = 0xC308C308u;
-constexpr float kOffset = 136.0f;           // 128 (bf16 base) + 8 (nibble bias)
-constexpr int kCounterBytes = 65536;        // split-K arrival counters at the head of the workspace
-constexpr int kMaxStrips = kCounterBytes / 4;
-
-struct LinearArgs {
-  const uint16_t* x;   // bf16 activations [M, K], row stride ldx (elements)
+// One projection of a launch, as the device sees it.
+struct Problem {
+  const uint16_t* x;   // bf16 [M, K], row stride ldx elements
   int64_t ldx;
-  const uint8_t* packed;  // [K/2, N], row stride ldp (bytes)
+  const uint8_t* packed;  // [K/2, N], row stride ldp bytes
   int64_t ldp;
-  const float* scale;  // [K/128, N], row stride lds (elements)
+  const float* scale;  // [K/128, N], row stride lds elements
   int64_t lds;
-  uint16_t* y;         // bf16 output [M, N], row stride ldy (elements)
+  uint16_t* y;         // bf16 [M, N], row stride ldy elements
   int64_t ldy;
-  int M, N, K;
-  float* part;         // split-K partials [nsplit][M][N] (skinny) / row sums [K/128][M] (gemm)
-  uint32_t* counters;  // one arrival counter per column strip, zero between calls
-  int gps;             // groups per split (skinny)
-  int nsplit;          // number of K splits (skinny)
-  int vec;             // bit 0: packed/scale rows 16B aligned; bit 1: x rows 16B aligned;
-                       // bit 2: y rows 8B aligned
-  int mtiles, ntiles;  // gemm tile grid
+  float* part;         // split-K partials [nsplit][M][N] (workspace)
+  uint32_t* counters;  // one arrival counter per strip / tile (workspace, zero between calls)
+  float* rowsum;       // gemm: 136 * row sums [K/128][M] (workspace, maybe shared)
+  int N, K;
+  int wg_begin;        // first workgroup of this problem in the launch grid
+  int rs_begin;        // rowsum_kernel: first workgroup (-1: row sums shared with another problem)
+  int tiles_m, tiles_n;  // gemm tile grid; gemv/skinny: tiles_n = column strips
+  int nsplit, gps;     // K split: nsplit ranges of gps groups
+  int red_begin;       // splitk_reduce_kernel: first workgroup of this problem
+  int vec;             // bit 0: packed and scale rows 16-byte aligned; bit 1: x rows 16-byte
+                       // aligned; bit 2: y rows 8-byte aligned
+};
+
+struct Launch {
+  Problem p[kMaxProblems];
+  int count;
+  int M;
+  int total_wgs;
 #ifdef W4A16_EXP
   uint64_t* trace;     // per-wave phase timestamps (experiments only)
 #endif
 };
 
 #ifdef W4A16_EXP
-#define W4A16_MARK(i)                                                                                       \
-  do {                                                                                                      \
-    if (a.trace && (threadIdx.x & 63) == 0)                                                                 \
-      a.trace[(((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6)) * 8 + \
-              (i)] = __builtin_amdgcn_s_memrealtime();                                                      \
+#define W4A16_MARK(i)                                                                                     \
+  do {                                                                                                    \
+    if (L.trace && (threadIdx.x & 63) == 0)                                                               \
+      L.trace[((size_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * 8 + (i)] =                  \
+          __builtin_amdgcn_s_memrealtime();                                                               \
   } while (0)
 #else
 #define W4A16_MARK(i) \
@@ -82,137 +79,87 @@ struct LinearArgs {
   } while (0)
 #endif
 
-__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
-  return __uint_as_float((uint32_t)h << 16);
+// Problem owning workgroup `wg` (wave-uniform scan of <= 8 entries).
+__device__ __forceinline__ int problem_of(const Launch& L, int wg) {
+  int p = 0;
+  for (int i = 1; i < L.count; ++i)
+    if (wg >= L.p[i].wg_begin) p = i;
+  return p;
 }
 
-// Round-to-nearest-even fp32 -> bf16; NaN becomes the canonical quiet NaN 0x7FC0,
-// the same rule torch uses for float -> bfloat16.
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
-
-__device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// A 32-bit word of packed bytes (4 columns) prepared for pair extraction.
-struct Prep {
-  uint32_t p;  // nibble sign bits flipped: every nibble now holds u = q + 8
-  uint32_t q;  // p >> 4: the high nibble of byte c sits in the low nibble of byte c
-};
-
-__device__ __forceinline__ Prep prep(uint32_t raw) {
-  Prep w;
-  w.p = raw ^ 0x88888888u;
-  w.q = w.p >> 4;
-  return w;
-}
-
-// bf16 pair for column c (0..3) of a prepared word: low half 128 + u(even row),
-// high half 128 + u(odd row).
-template <int C>
-__device__ __forceinline__ uint32_t pair_of(Prep w) {
-  // v_perm_b32 byte pool: bytes 0-3 come from the second operand, 4-7 from the first.
-  const uint32_t y = __builtin_amdgcn_perm(w.p, w.q, (uint32_t)C | ((uint32_t)(4 + C) << 16));
-  return (y & 0x000F000Fu) | kBf16Base;
-}
-
-__device__ __forceinline__ uint32_t pair_dyn(Prep w, int c) {
-  switch (c) {
-    case 0: return pair_of<0>(w);
-    case 1: return pair_of<1>(w);
-    case 2: return pair_of<2>(w);
-    default: return pair_of<3>(w);
+// ---------------------------------------------------------------------------
+// Split-K finish shared by the M <= 32 kernels.  Each workgroup publishes its
+// fp32 partial for (split, strip) with agent-coherent stores (no whole-L2
+// writeback / invalidate, which an agent-scope release/acquire fence costs on
+// this chip).  Every wave waits for its stores to be acknowledged before the
+// barrier, so when thread 0 bumps the strip's arrival counter all partials of
+// the workgroup are visible device-wide.  The last arrival, whose counter
+// update has returned before it issues any load, sums the partials in split
+// order (deterministic), writes bf16 and resets the counter to zero.  Partials
+// are loaded 8 at a time so their latencies overlap.
+// ---------------------------------------------------------------------------
+template <int NT, class PartialFn>
+__device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split, int strip, int n0, int wcols,
+                                              int rows, PartialFn partial) {
+  const int N = P.N;
+  const int elems = rows * wcols;
+  float* part = P.part + (size_t)split * M * N;
+  for (int e = threadIdx.x; e < elems; e += NT) {
+    const int m = e / wcols, c = e % wcols, n = n0 + c;
+    if (n < N) store_coherent(part + (size_t)m * N + n, partial(e));
   }
-}
-
-// Raw buffer resource over [base, base + bytes): untyped dword loads
-// (DATA_FORMAT 32 in the third descriptor word), no stride.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-template <int BYTES>
-__device__ __forceinline__ void buffer_load_packed(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
-                                                   uint32_t (&out)[BYTES / 4]) {
-  if constexpr (BYTES == 16) {
-    const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-    out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
-  } else if constexpr (BYTES == 8) {
-    const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
-    out[0] = v[0]; out[1] = v[1];
-  } else {
-    out[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+  wait_vmem();
+  __syncthreads();
+  __shared__ int is_last;
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(P.counters + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (prev == (uint32_t)(P.nsplit - 1));
   }
-}
-
-// Load `bytes` (4, 8 or 16) consecutive packed bytes starting at column `col`
-// of one packed row.  Columns at or beyond N read as 0 (q = 0).
-// FULL: the caller guarantees the whole tile is in bounds and aligned, so the
-// load is unconditional (no per-lane branch; all loads of a group can be in
-// flight together).
-template <int BYTES, bool FULL>
-__device__ __forceinline__ void load_packed(const uint8_t* row, int col, int N, bool vec,
-                                            uint32_t (&out)[BYTES / 4]) {
-  if (FULL || (vec && col + BYTES <= N)) {
-    if constexpr (BYTES == 16) {
-      u32x4_t v = *reinterpret_cast<const u32x4_t*>(row + col);
-      out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
-    } else if constexpr (BYTES == 8) {
-      u32x2_t v = *reinterpret_cast<const u32x2_t*>(row + col);
-      out[0] = v[0]; out[1] = v[1];
-    } else {
-      out[0] = *reinterpret_cast<const uint32_t*>(row + col);
-    }
-  } else {
+  __syncthreads();
+  if (!is_last) return;
+  for (int e = threadIdx.x; e < elems; e += NT) {
+    const int m = e / wcols, c = e % wcols, n = n0 + c;
+    if (n < N) {
+      const float* src = P.part + (size_t)m * N + n;
+      const size_t stride = (size_t)M * N;
+      float v = 0.f;
+      for (int sp0 = 0; sp0 < P.nsplit; sp0 += 8) {
+        float t[8];
 #pragma unroll
-    for (int w = 0; w < BYTES / 4; ++w) {
-      uint32_t acc = 0;
+        for (int i = 0; i < 8; ++i) t[i] = sp0 + i < P.nsplit ? load_coherent(src + (size_t)(sp0 + i) * stride) : 0.f;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int c = col + 4 * w + b;
-        const uint32_t v = (c < N) ? (uint32_t)row[c] : 0u;
-        acc |= v << (8 * b);
+        for (int i = 0; i < 8; ++i) v += t[i];
       }
-      out[w] = acc;
+      P.y[(int64_t)m * P.ldy + n] = f32_to_bf16(v);
     }
   }
+  if (threadIdx.x == 0) __hip_atomic_store(P.counters + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Load `CNT` consecutive fp32 scales from column `col`; columns >= N read 0.
-template <int CNT, bool FULL>
-__device__ __forceinline__ void load_scales(const float* row, int col, int N, bool vec, float (&s)[CNT]) {
-  if (FULL || (vec && col + CNT <= N)) {
-#pragma unroll
-    for (int i = 0; i < CNT; i += 4) {
-      f32x4_t v = *reinterpret_cast<const f32x4_t*>(row + col + i);
-      s[i] = v[0]; s[i + 1] = v[1]; s[i + 2] = v[2]; s[i + 3] = v[3];
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < CNT; ++i) s[i] = (col + i < N) ? row[col + i] : 0.0f;
-  }
-}
-
-// 8 consecutive bf16 activations of one row (16 bytes).
-__device__ __forceinline__ bf16x8_t load_x8(const uint16_t* p, bool vec) {
-  if (vec) return *reinterpret_cast<const bf16x8_t*>(p);
-  u32x4_t v;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = (uint32_t)p[2 * i] | ((uint32_t)p[2 * i + 1] << 16);
-  return as_bf16x8(v);
-}
-
+// ---------------------------------------------------------------------------
+// Decode GEMV kernel (M <= 16): the HBM-bound path of batch-1 decode.
+//
+// Lane mapping (shared with skinny_kernel): a wave owns 16*CPL output columns;
+// lane l covers columns col0 = n0 + CPL*(l%16) .. +CPL and, inside each 32-row
+// K step, rows 8*(l/16) .. +8, i.e. four packed rows.  Per 128-row group a
+// lane issues 16 loads of CPL bytes (4 steps x 4 packed rows).  Column t of the
+// lane is MFMA instance t with virtual column l%16, so a lane's CPL outputs
+// are contiguous.  Per group:
+//   acc = -136 * sum_k x   (4 MFMAs against a constant -136 operand),
+//   acc += x . (q + 136)   (4 K steps x CPL MFMAs),   total += acc * scale.
+//
+// Workgroup = 4 waves on one strip; blockIdx selects (problem, split, strip)
+// and each wave takes one of the split's gps (=4) groups.  The register budget
+// (one group in flight per wave, buffer loads with scalar row offsets) allows
+// 3 workgroups per CU, so decode-sized grids are resident in a single round.
+// A wave first issues its group's weight and scale loads, then the workgroup
+// copies its activations x[0:M, krange] into LDS, and A fragments are read
+// from LDS at the step that needs them.
+// ---------------------------------------------------------------------------
 template <int CPL>
 struct DecodeSlot {
   static constexpr int WPR = CPL / 4;
-  uint32_t raw[4][4][WPR];
+  uint32_t raw[4][4][WPR];  // [K step][packed row][word]
   float s[CPL];
 };
 
@@ -255,307 +202,39 @@ __device__ __forceinline__ void decode_compute(const DecodeSlot<CPL>& d, const u
     for (int r = 0; r < 4; ++r) total[t][r] = __builtin_fmaf(acc[t][r], d.s[t], total[t][r]);
 }
 
-// ---------------------------------------------------------------------------
-// Split-K finish shared by the M <= 32 kernels.  Each workgroup publishes its
-// fp32 partial for (split, strip) with agent-scope relaxed atomic stores, which
-// the hardware keeps coherent per access across the XCD L2s (no whole-L2
-// writeback / invalidate as a release/acquire fence would need).  The
-// workgroup barrier waits until those stores are acknowledged before thread 0
-// bumps the strip's arrival counter; the last arrival, whose counter update
-// has returned before it issues any load, sums all partials in split order
-// (deterministic), writes bf16 and resets the counter to zero.  Partials are
-// loaded 8 at a time so their latencies overlap.
-// ---------------------------------------------------------------------------
-template <int NT, class PartialFn>
-__device__ __forceinline__ void splitk_finish(const LinearArgs& a, int strip, int n0, int wcols, int rows,
-                                              PartialFn partial) {
-  const int M = a.M, N = a.N;
-  const int elems = rows * wcols;
-  float* part = a.part + (size_t)blockIdx.y * M * N;
-  for (int e = threadIdx.x; e < elems; e += NT) {
-    const int m = e / wcols, c = e % wcols, n = n0 + c;
-    if (n < N) __hip_atomic_store(part + (size_t)m * N + n, partial(e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  __shared__ int is_last;
-  if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(a.counters + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (prev == (uint32_t)(a.nsplit - 1));
-  }
-  __syncthreads();
-  if (!is_last) return;
-  for (int e = threadIdx.x; e < elems; e += NT) {
-    const int m = e / wcols, c = e % wcols, n = n0 + c;
-    if (n < N) {
-      const float* src = a.part + (size_t)m * N + n;
-      const size_t stride = (size_t)M * N;
-      float v = 0.f;
-      for (int sp0 = 0; sp0 < a.nsplit; sp0 += 8) {
-        float t[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          t[i] = sp0 + i < a.nsplit ? __hip_atomic_load(src + (size_t)(sp0 + i) * stride, __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT)
-                                    : 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v += t[i];
-      }
-      a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(v);
-    }
-  }
-  if (threadIdx.x == 0) __hip_atomic_store(a.counters + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// ---------------------------------------------------------------------------
-// Skinny kernel (M <= 32).
-//
-// A wave owns 16*CPL output columns and a set of 128-row K groups.  Lane l
-// covers columns col0 = n0 + CPL*(l%16) .. +CPL and, inside each 32-row K step,
-// rows 8*(l/16) .. +8 (four packed rows).  Per group a lane issues 16 loads of
-// CPL bytes (4 steps x 4 packed rows); 16 lanes read CPL*16 contiguous bytes of
-// one packed row, so each wave load instruction covers four full row segments.
-// Column t of the lane maps to MFMA instance t with virtual column l%16, so the
-// lane's CPL output columns are contiguous.  MT M-subtiles of 16 rows reuse the
-// same unpacked weights.
-//
-// Per group g and M-subtile:  acc = -136*sum_k x  (4 MFMAs against a -136 matrix),
-// acc += x . (q + 136) over the 4 K steps, total += acc * scale[g, n].
-// A wave keeps the next group's loads in flight while it computes the current
-// one.
-//
-// The WAVES waves of a workgroup split the workgroup's groups round-robin and
-// are summed through LDS.  Workgroups along gridDim.y split K further; each
-// writes an fp32 partial and the last one to arrive for a column strip (arrival
-// counter) adds the partials in split order and writes bf16.  The counter is
-// reset to zero by that last workgroup, so the workspace needs zeroing once.
-// ---------------------------------------------------------------------------
-template <int MT, int CPL>
-struct SkinnyGroup {
-  static constexpr int WPR = CPL / 4;
-  uint32_t raw[4][4][WPR];  // [K step][packed row][word]
-  bf16x8_t A[MT][4];        // [M subtile][K step]
-  float s[CPL];             // scales of the lane's columns
-};
-
-template <int MT, int CPL, bool FULL>
-__device__ __forceinline__ void skinny_load(const LinearArgs& a, int g, int col0, int mrow0, int lk,
-                                            uint32_t keep0, SkinnyGroup<MT, CPL>& d) {
-  constexpr int WPR = CPL / 4;
-  const bool vec_w = (a.vec & 1) != 0;
-  const bool vec_x = (a.vec & 2) != 0;
-#pragma unroll
-  for (int st = 0; st < 4; ++st)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
-#ifdef W4A16_EXP_NOLOAD
-#pragma unroll
-      for (int w = 0; w < WPR; ++w) d.raw[st][r][w] = (uint32_t)(col0 * 2654435761u + pr * 97u + w);
-#else
-      load_packed<CPL, FULL>(a.packed + pr * a.ldp, col0, a.N, vec_w, d.raw[st][r]);
-#endif
-    }
-  // Activations: lane holds x[m][g*128 + 32*st + 8*lk .. +8] for m = 16*mt + l%16.
-  // Rows past M load row M-1 (always valid) and are zeroed by a select, so the
-  // loads carry no per-lane branch.
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = mrow0 + 16 * mt;
-    const int mrow = m < a.M ? m : a.M - 1;
-    const uint32_t keep = mt == 0 ? keep0 : (m < a.M ? 0xffffffffu : 0u);
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      u32x4_t v = __builtin_bit_cast(
-          u32x4_t, load_x8(a.x + (int64_t)mrow * a.ldx + (int64_t)g * kGroup + st * 32 + lk * 8, vec_x));
-      d.A[mt][st] = as_bf16x8(v & keep);
-    }
-  }
-  load_scales<CPL, FULL>(a.scale + (int64_t)g * a.lds, col0, a.N, vec_w, d.s);
-  (void)WPR;
-}
-
-template <int MT, int CPL>
-__device__ __forceinline__ void skinny_compute(const SkinnyGroup<MT, CPL>& d, f32x4_t (&total)[MT][CPL]) {
-  constexpr int WPR = CPL / 4;
-#ifdef W4A16_EXP_LOADONLY
-  uint32_t h = 0;
-  for (int st = 0; st < 4; ++st) for (int r = 0; r < 4; ++r) for (int w = 0; w < WPR; ++w) h ^= d.raw[st][r][w];
-  total[0][0][0] += __uint_as_float(h & 0x3fffffu) + (float)d.A[0][0][0] + d.s[0];
-  return;
-#endif
-  const bf16x8_t neg136 = as_bf16x8(u32x4_t{kBf16Neg136, kBf16Neg136, kBf16Neg136, kBf16Neg136});
-  // Offset correction -136 * sum_{k in group} x[m, k], in MFMA output layout.
-  f32x4_t cinit[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < 4; ++st) c = mfma16(d.A[mt][st], neg136, c);
-    cinit[mt] = c;
-  }
-  // Step-outer: the CPL column accumulators of a step are independent MFMAs.
-  f32x4_t acc[MT][CPL];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-#pragma unroll
-    for (int wi = 0; wi < WPR; ++wi) {
-      Prep pw[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pw[r] = prep(d.raw[st][r][wi]);
-#pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) {
-        const int t = wi * 4 + c4;
-        const bf16x8_t B = as_bf16x8(u32x4_t{pair_dyn(pw[0], c4), pair_dyn(pw[1], c4),
-                                             pair_dyn(pw[2], c4), pair_dyn(pw[3], c4)});
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][t] = mfma16(d.A[mt][st], B, st == 0 ? cinit[mt] : acc[mt][t]);
-      }
-    }
-  }
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int t = 0; t < CPL; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) total[mt][t][r] = __builtin_fmaf(acc[mt][t][r], d.s[t], total[mt][t][r]);
-}
-
-template <int MT, int CPL, int WAVES, bool FULL, bool PIPE>
-__global__ __launch_bounds__(WAVES * 64) void skinny_kernel(LinearArgs a) {
-  constexpr int WCOLS = 16 * CPL;    // columns per wave / workgroup
-  constexpr int NT = WAVES * 64;
-  extern __shared__ float red[];     // [WAVES][R rows][WCOLS]
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int lc = lane & 15;
-  const int lk = lane >> 4;
-  const int strip = blockIdx.x;
-  const int n0 = strip * WCOLS;
-  const int col0 = n0 + lc * CPL;
-  const int G = a.K / kGroup;
-  const int g_begin = blockIdx.y * a.gps;
-  const int g_end = min(G, g_begin + a.gps);
-  const int M = a.M;
-  const int N = a.N;
-  const uint32_t keep0 = lc < M ? 0xffffffffu : 0u;
-
-  W4A16_MARK(0);
-  f32x4_t total[MT][CPL];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int t = 0; t < CPL; ++t) total[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  // This wave's groups are g = g_begin + wave, + WAVES, ...  With PIPE the
-  // next group's loads are issued before the current group is computed.
-  int g = g_begin + wave;
-  if (!PIPE) {
-    for (; g < g_end; g += WAVES) {
-      SkinnyGroup<MT, CPL> cur;
-      skinny_load<MT, CPL, FULL>(a, g, col0, lc, lk, keep0, cur);
-      W4A16_MARK(1);
-      skinny_compute<MT, CPL>(cur, total);
-    }
-  } else if (g < g_end) {
-    SkinnyGroup<MT, CPL> cur, nxt;
-    skinny_load<MT, CPL, FULL>(a, g, col0, lc, lk, keep0, cur);
-    while (true) {
-      const int gn = g + WAVES;
-      if (gn < g_end) skinny_load<MT, CPL, FULL>(a, gn, col0, lc, lk, keep0, nxt);
-      skinny_compute<MT, CPL>(cur, total);
-      if (gn >= g_end) break;
-      const int gnn = gn + WAVES;
-      if (gnn < g_end) skinny_load<MT, CPL, FULL>(a, gnn, col0, lc, lk, keep0, cur);
-      skinny_compute<MT, CPL>(nxt, total);
-      if (gnn >= g_end) break;
-      g = gnn;
-    }
-  }
-
-  W4A16_MARK(3);
-  // ---- reduce the waves through LDS (rows < M only) ----
-  const int R = min(M, 16 * MT);
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = mt * 16 + lk * 4 + r;
-      if (m < R) {
-        float* dst = red + ((size_t)wave * R + m) * WCOLS + lc * CPL;
-#pragma unroll
-        for (int t = 0; t < CPL; t += 4)
-          *reinterpret_cast<f32x4_t*>(dst + t) =
-              f32x4_t{total[mt][t][r], total[mt][t + 1][r], total[mt][t + 2][r], total[mt][t + 3][r]};
-      }
-    }
-  __syncthreads();
-  W4A16_MARK(4);
-
-  const int elems = R * WCOLS;
-  auto wave_sum = [&](int e) {
-    float v = red[e];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) v += red[(size_t)w * elems + e];
-    return v;
-  };
-  if (a.nsplit == 1) {
-    for (int e = threadIdx.x; e < elems; e += NT) {
-      const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
-      if (n < N) a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(wave_sum(e));
-    }
-    W4A16_MARK(5);
-    return;
-  }
-
-  splitk_finish<NT>(a, strip, n0, WCOLS, R, wave_sum);
-  W4A16_MARK(6);
-}
-
-// ---------------------------------------------------------------------------
-// Decode GEMV kernel (M <= 16): the HBM-bound path of batch-1 decode.
-//
-// Workgroup = 4 waves on one strip of 16*CPL columns; blockIdx.y selects a
-// range of gps groups (normally 4, one per wave).  Sized so that every
-// workgroup of a launch is resident at once: the lean register budget
-// (one group in flight per wave, 32-bit row offsets) allows 3+ workgroups per
-// CU, and launches are planned as whole multiples of the CU count where the
-// shape allows.  Order of work in a wave: issue the group's 16 weight loads
-// and its scales, copy the workgroup's activations x[0:M, krange] into LDS,
-// barrier, then unpack + MFMA with A fragments read from LDS.
-// Lane mapping and arithmetic are those of skinny_kernel.
-// ---------------------------------------------------------------------------
 template <int CPL, bool FULL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void gemv_kernel(LinearArgs a) {
-  constexpr int WPR = CPL / 4;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void gemv_kernel(Launch L) {
   constexpr int WCOLS = 16 * CPL;
   extern __shared__ __attribute__((aligned(16))) float smem[];
+
+  const int pi = problem_of(L, blockIdx.x);
+  const Problem& P = L.p[pi];
+  const int local = blockIdx.x - P.wg_begin;
+  const int strip = local % P.tiles_n;
+  const int split = local / P.tiles_n;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lc = lane & 15;
   const int lk = lane >> 4;
-  const int strip = blockIdx.x;
   const int n0 = strip * WCOLS;
   const int col0 = n0 + lc * CPL;
-  const int G = a.K / kGroup;
-  const int g_begin = blockIdx.y * a.gps;
-  const int g_end = min(G, g_begin + a.gps);
-  const int M = a.M, N = a.N;
+  const int M = L.M, N = P.N;
+  const int G = P.K / kGroup;
+  const int g_begin = split * P.gps;
+  const int g_end = min(G, g_begin + P.gps);
   const int kspan = (g_end - g_begin) * kGroup;
-  const int kpitch = a.gps * kGroup + 8;   // +16 B per row against LDS bank conflicts
-  const bool vec_w = (a.vec & 1) != 0;
+  const int kpitch = P.gps * kGroup + 8;  // +16 B per row against LDS bank conflicts
   W4A16_MARK(0);
 
-  // Weight loads for this wave's group.  FULL launches use buffer loads: the
-  // per-lane offset (column, k-block row) is fixed and the row of each load
-  // is a scalar offset, so no per-load address arithmetic is needed.
+  // Weight + scale loads for this wave's group.  FULL launches use buffer loads
+  // whose per-lane offset (column, k-block row) is fixed and whose row is a
+  // scalar offset, so no per-load address arithmetic is needed.
   int g = g_begin + wave;
   DecodeSlot<CPL> cur;
-  const uint32_t ldp = (uint32_t)a.ldp;
-  // (Only FULL launches use these; the resources are harmless otherwise.)
-  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.packed, (uint32_t)((size_t)(a.K / 2) * a.ldp));
-  const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.scale, (uint32_t)((size_t)G * a.lds * 4));
+  const uint32_t ldp = (uint32_t)P.ldp;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(P.packed, (uint32_t)((size_t)(P.K / 2) * P.ldp));
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(P.scale, (uint32_t)((size_t)G * P.lds * 4));
   const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
   const uint32_t svoff = (uint32_t)col0 * 4u;
   auto load_group = [&](int gg) {
@@ -565,23 +244,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
       for (int st = 0; st < 4; ++st)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          buffer_load_packed<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, cur.raw[st][r]);
-      const uint32_t soff = (uint32_t)gg * (uint32_t)a.lds * 4u;
+          buffer_load_bytes<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, cur.raw[st][r]);
+      const uint32_t soff = (uint32_t)gg * (uint32_t)P.lds * 4u;
 #pragma unroll
       for (int t = 0; t < CPL; t += 4) {
-        const f32x4_t v = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, svoff + 4u * t, soff, 0));
+        const f32x4_t v =
+            __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, svoff + 4u * t, soff, 0));
         cur.s[t] = v[0]; cur.s[t + 1] = v[1]; cur.s[t + 2] = v[2]; cur.s[t + 3] = v[3];
       }
     } else {
-      const uint8_t* base = a.packed + (int64_t)gg * kPackedRowsPerGroup * a.ldp;
+      const uint8_t* base = P.packed + (int64_t)gg * kPackedRowsPerGroup * P.ldp;
 #pragma unroll
       for (int st = 0; st < 4; ++st)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t off = (uint32_t)((st * 16 + lk * 4 + r) * ldp);
-          load_packed<CPL, FULL>(base + off, col0, N, vec_w, cur.raw[st][r]);
-        }
-      load_scales<CPL, FULL>(a.scale + (int64_t)gg * a.lds, col0, N, vec_w, cur.s);
+        for (int r = 0; r < 4; ++r)
+          load_packed<CPL, false>(base + (int64_t)(st * 16 + lk * 4 + r) * P.ldp, col0, N, (P.vec & 1) != 0,
+                                  cur.raw[st][r]);
+      load_scales<CPL, false>(P.scale + (int64_t)gg * P.lds, col0, N, (P.vec & 1) != 0, cur.s);
     }
   };
   if (g < g_end) load_group(g);
@@ -590,17 +269,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
   // Activations of the workgroup's K range -> LDS.
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
   {
-    const bool vec_x = (a.vec & 2) != 0;
+    const bool vec_x = (P.vec & 2) != 0;
     const int chunks = kspan / 8;
     for (int i = threadIdx.x; i < M * chunks; i += 256) {
       const int m = i / chunks, c = i % chunks;
-      const uint16_t* src = a.x + (int64_t)m * a.ldx + (int64_t)g_begin * kGroup + c * 8;
+      const uint16_t* src = P.x + (int64_t)m * P.ldx + (int64_t)g_begin * kGroup + c * 8;
       *reinterpret_cast<u32x4_t*>(xs + m * kpitch + c * 8) = __builtin_bit_cast(u32x4_t, load_x8(src, vec_x));
     }
   }
   __syncthreads();
   W4A16_MARK(2);
 
+  // Lanes of rows past M read row M-1 and zero it.
   const uint32_t keep = lc < M ? 0xffffffffu : 0u;
   const int xrow_idx = lc < M ? lc : M - 1;
   f32x4_t total[CPL];
@@ -632,35 +312,172 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
   auto wave_sum = [&](int e) {
     return ((red[e] + red[(size_t)elems + e]) + red[(size_t)2 * elems + e]) + red[(size_t)3 * elems + e];
   };
-  if (a.nsplit == 1) {
+  if (P.nsplit == 1) {
     for (int e = threadIdx.x; e < elems; e += 256) {
       const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
-      if (n < N) a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(wave_sum(e));
+      if (n < N) P.y[(int64_t)m * P.ldy + n] = f32_to_bf16(wave_sum(e));
     }
     W4A16_MARK(5);
     return;
   }
-  splitk_finish<256>(a, strip, n0, WCOLS, M, wave_sum);
+  splitk_finish<256>(P, M, split, strip, n0, WCOLS, M, wave_sum);
   W4A16_MARK(6);
-  (void)WPR;
 }
 
 // ---------------------------------------------------------------------------
-// Row sums for the gemm offset correction: out[g*M + m] = 136 * sum_{k in g} x[m,k].
-// 16 lanes per (row, group); each lane sums 8 values, then a butterfly over the
-// 16 lanes (fixed order, deterministic).
+// Skinny kernel (16 < M <= 32, one problem).  Lane mapping and arithmetic as
+// gemv_kernel with two 16-row M subtiles sharing each unpacked B fragment;
+// activations come straight from global memory (rows past M zeroed by a
+// select), and the 4 waves of a workgroup take the split's groups round-robin.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void rowsum_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M,
-                                                     int K, int vec_x, float* __restrict__ out) {
-  const int G = K / kGroup;
-  const int64_t item = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+constexpr int kSkinnyCPL = 8;
+
+struct SkinnyGroup {
+  uint32_t raw[4][4][kSkinnyCPL / 4];
+  bf16x8_t A[2][4];  // [M subtile][K step]
+  float s[kSkinnyCPL];
+};
+
+template <bool FULL>
+__device__ __forceinline__ void skinny_load(const Problem& P, int M, int g, int col0, int lc, int lk, SkinnyGroup& d) {
+  const bool vec_x = (P.vec & 2) != 0;
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
+      load_packed<kSkinnyCPL, FULL>(P.packed + pr * P.ldp, col0, P.N, (P.vec & 1) != 0, d.raw[st][r]);
+    }
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int m = lc + 16 * mt;
+    const int mrow = m < M ? m : M - 1;
+    const uint32_t keep = m < M ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const u32x4_t v = __builtin_bit_cast(
+          u32x4_t, load_x8(P.x + (int64_t)mrow * P.ldx + (int64_t)g * kGroup + st * 32 + lk * 8, vec_x));
+      d.A[mt][st] = as_bf16x8(v & keep);
+    }
+  }
+  load_scales<kSkinnyCPL, FULL>(P.scale + (int64_t)g * P.lds, col0, P.N, (P.vec & 1) != 0, d.s);
+}
+
+__device__ __forceinline__ void skinny_compute(const SkinnyGroup& d, f32x4_t (&total)[2][kSkinnyCPL]) {
+  constexpr int WPR = kSkinnyCPL / 4;
+  const bf16x8_t neg136 = as_bf16x8(u32x4_t{kBf16Neg136, kBf16Neg136, kBf16Neg136, kBf16Neg136});
+  f32x4_t cinit[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) c = mfma16(d.A[mt][st], neg136, c);
+    cinit[mt] = c;
+  }
+  f32x4_t acc[2][kSkinnyCPL];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+#pragma unroll
+    for (int wi = 0; wi < WPR; ++wi) {
+      Prep pw[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pw[r] = prep(d.raw[st][r][wi]);
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) {
+        const int t = wi * 4 + c4;
+        const bf16x8_t B = as_bf16x8(u32x4_t{pair_dyn(pw[0], c4), pair_dyn(pw[1], c4),
+                                             pair_dyn(pw[2], c4), pair_dyn(pw[3], c4)});
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) acc[mt][t] = mfma16(d.A[mt][st], B, st == 0 ? cinit[mt] : acc[mt][t]);
+      }
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int t = 0; t < kSkinnyCPL; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) total[mt][t][r] = __builtin_fmaf(acc[mt][t][r], d.s[t], total[mt][t][r]);
+}
+
+template <bool FULL>
+__global__ __launch_bounds__(256) void skinny_kernel(Launch L) {
+  constexpr int WCOLS = 16 * kSkinnyCPL;
+  extern __shared__ __attribute__((aligned(16))) float smem[];  // [4 waves][M][WCOLS]
+  const Problem& P = L.p[0];
+  const int strip = blockIdx.x % P.tiles_n;
+  const int split = blockIdx.x / P.tiles_n;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lc = lane & 15;
+  const int lk = lane >> 4;
+  const int n0 = strip * WCOLS;
+  const int col0 = n0 + lc * kSkinnyCPL;
+  const int M = L.M, N = P.N;
+  const int G = P.K / kGroup;
+  const int g_begin = split * P.gps;
+  const int g_end = min(G, g_begin + P.gps);
+
+  f32x4_t total[2][kSkinnyCPL];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int t = 0; t < kSkinnyCPL; ++t) total[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int g = g_begin + wave; g < g_end; g += 4) {
+    SkinnyGroup cur;
+    skinny_load<FULL>(P, M, g, col0, lc, lk, cur);
+    skinny_compute(cur, total);
+  }
+
+  float* red = smem;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = mt * 16 + lk * 4 + r;
+      if (m < M) {
+        float* dst = red + ((size_t)wave * M + m) * WCOLS + lc * kSkinnyCPL;
+#pragma unroll
+        for (int t = 0; t < kSkinnyCPL; t += 4)
+          *reinterpret_cast<f32x4_t*>(dst + t) =
+              f32x4_t{total[mt][t][r], total[mt][t + 1][r], total[mt][t + 2][r], total[mt][t + 3][r]};
+      }
+    }
+  __syncthreads();
+  const int elems = M * WCOLS;
+  auto wave_sum = [&](int e) {
+    return ((red[e] + red[(size_t)elems + e]) + red[(size_t)2 * elems + e]) + red[(size_t)3 * elems + e];
+  };
+  if (P.nsplit == 1) {
+    for (int e = threadIdx.x; e < elems; e += 256) {
+      const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
+      if (n < N) P.y[(int64_t)m * P.ldy + n] = f32_to_bf16(wave_sum(e));
+    }
+    return;
+  }
+  splitk_finish<256>(P, M, split, strip, n0, WCOLS, M, wave_sum);
+}
+
+// ---------------------------------------------------------------------------
+// Row sums for the gemm offset correction: rowsum[g*M + m] = 136 * sum_{k in g} x[m,k].
+// 16 lanes per (row, group); each lane sums 8 values, then a butterfly over the
+// 16 lanes (fixed order, deterministic).  Problems that share x share the sums.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rowsum_kernel(Launch L) {
+  int pi = 0;
+  for (int i = 0; i < L.count; ++i)
+    if (L.p[i].rs_begin >= 0 && (int)blockIdx.x >= L.p[i].rs_begin) pi = i;
+  const Problem& P = L.p[pi];
+  const int M = L.M;
+  const int G = P.K / kGroup;
+  const int64_t item = (int64_t)(blockIdx.x - P.rs_begin) * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
   const bool valid = item < (int64_t)M * G;
   const int m = valid ? (int)(item / G) : 0;
   const int g = valid ? (int)(item % G) : 0;
   float s = 0.f;
   if (valid) {
-    const bf16x8_t v = load_x8(x + (int64_t)m * ldx + (int64_t)g * kGroup + sub * 8, vec_x != 0);
+    const bf16x8_t v = load_x8(P.x + (int64_t)m * P.ldx + (int64_t)g * kGroup + sub * 8, (P.vec & 2) != 0);
     const u32x4_t w = __builtin_bit_cast(u32x4_t, v);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -670,30 +487,33 @@ __global__ __launch_bounds__(256) void rowsum_kernel(const uint16_t* __restrict_
   }
 #pragma unroll
   for (int off = 8; off >= 1; off >>= 1) s += __shfl_xor(s, off, 16);
-  if (valid && sub == 0) out[(int64_t)g * M + m] = kOffset * s;
+  if (valid && sub == 0) P.rowsum[(int64_t)g * M + m] = kOffset * s;
 }
 
 // ---------------------------------------------------------------------------
 // GEMM kernel (M > 32).
 //
-// Workgroup tile 128 rows x 256 columns, 4 waves side by side along N, each
-// wave 128 x 64 (8 M-subtiles x 4 MFMA column blocks, 4 columns per lane).
+// Workgroup tile 128 rows x 64*CPL columns, 4 waves side by side along N, each
+// wave 128 x 16*CPL (8 M-subtiles x CPL MFMA column blocks, CPL columns per
+// lane: 4 for wide problems, 2 to double the tile count of narrow ones).
 // Per 128-row K group:
 //  * the activation tile (128 x 128 bf16, 32 KB) is copied global -> LDS with
 //    direct-to-LDS loads in MFMA fragment order (wave w copies K step w),
 //    double buffered, together with the group's 128 row sums (rowsum_kernel);
-//  * each wave loads its own packed weights (16 buffer loads of 4 bytes,
+//  * each wave loads its own packed weights (16 buffer loads of CPL bytes,
 //    scalar row offsets) and scales one group ahead, in registers;
 //  * running-ratio fold: the accumulator U is kept in units of the current
-//    group's scale, U <- U * (s_prev / s) - 136 * rowsum, so one fp32
-//    accumulator set suffices and the MFMAs accumulate straight into it;
-//    the output is U * s_last (see clamp_scale for zero / tiny scales).
-// Tiles are handed out XCD-major: workgroup b runs on XCD b % 8, and each XCD
-// receives a contiguous range of tile ids, ordered in column bands of 4 row
-// tiles, so the rows of x and the weight columns an XCD touches stay in its L2.
+//    group's scale, U <- U * (s_prev / s) - 136 * rowsum, so a single fp32
+//    accumulator set suffices and the MFMAs accumulate straight into it; the
+//    output is U * s_last (see clamp_scale for zero / tiny scales).
+// blockIdx -> (problem, K split, tile).  Tiles are handed out XCD-major:
+// workgroup b runs on XCD b % 8 and each XCD receives a contiguous range of
+// work ids, ordered within a problem in column bands of 4 row tiles, so the
+// rows of x and the weight columns an XCD touches stay in its L2.  With K
+// split, each split publishes an fp32 partial tile and the last arrival per
+// tile sums them in split order (as splitk_finish).
 // ---------------------------------------------------------------------------
 constexpr int kGemmRows = 128;
-constexpr int kGemmCols = 256;
 constexpr int kGemmMT = 8;      // 16-row subtiles per wave
 constexpr int kGemmBand = 4;    // row tiles per column band
 
@@ -706,48 +526,72 @@ __device__ __forceinline__ float clamp_scale(float s) {
   return a < 1e-20f ? __builtin_copysignf(1e-20f, s) : s;
 }
 
-template <bool FULL>
-#ifndef W4A16_GEMM_WAVES
-#define W4A16_GEMM_WAVES 2
-#endif
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W4A16_GEMM_WAVES, 8))) void gemm_kernel(LinearArgs a) {
+// B fragments of one K step: raw[r] holds packed row r's CPL bytes.  For CPL=2
+// two rows share a word (row 2j in the low half, row 2j+1 in the high half).
+template <int CPL>
+__device__ __forceinline__ void gemm_unpack(const uint32_t (&raw)[4], bf16x8_t (&B)[CPL]) {
+  if constexpr (CPL == 4) {
+    Prep p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = prep(raw[r]);
+    B[0] = as_bf16x8(u32x4_t{pair_of<0>(p[0]), pair_of<0>(p[1]), pair_of<0>(p[2]), pair_of<0>(p[3])});
+    B[1] = as_bf16x8(u32x4_t{pair_of<1>(p[0]), pair_of<1>(p[1]), pair_of<1>(p[2]), pair_of<1>(p[3])});
+    B[2] = as_bf16x8(u32x4_t{pair_of<2>(p[0]), pair_of<2>(p[1]), pair_of<2>(p[2]), pair_of<2>(p[3])});
+    B[3] = as_bf16x8(u32x4_t{pair_of<3>(p[0]), pair_of<3>(p[1]), pair_of<3>(p[2]), pair_of<3>(p[3])});
+  } else {
+    const Prep p01 = prep(raw[0] | (raw[1] << 16));
+    const Prep p23 = prep(raw[2] | (raw[3] << 16));
+    B[0] = as_bf16x8(u32x4_t{pair_of<0>(p01), pair_of<2>(p01), pair_of<0>(p23), pair_of<2>(p23)});
+    B[1] = as_bf16x8(u32x4_t{pair_of<1>(p01), pair_of<3>(p01), pair_of<1>(p23), pair_of<3>(p23)});
+  }
+}
+
+template <int CPL, bool FULL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void gemm_kernel(Launch L) {
+  constexpr int WCOLS = 16 * CPL;       // columns per wave
   __shared__ u32x4_t As[2][4 * kGemmMT * 64];  // [buf][step][subtile][lane] 16 B each
   __shared__ __attribute__((aligned(16))) float Cs[2][kGemmRows];
+
+  // ---- work assignment ----
+  int wid = blockIdx.x;
+  if ((gridDim.x & 7) == 0) {
+    const int per_xcd = gridDim.x >> 3;
+    wid = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  }
+  if (wid >= L.total_wgs) return;
+  const int pi = problem_of(L, wid);
+  const Problem& P = L.p[pi];
+  const int tiles = P.tiles_m * P.tiles_n;
+  const int local = wid - P.wg_begin;
+  const int split = local / tiles;
+  const int tile_lin = local % tiles;
+  const int band_size = kGemmBand * P.tiles_n;
+  const int band = tile_lin / band_size;
+  const int first_m = band * kGemmBand;
+  const int band_rows = min(kGemmBand, P.tiles_m - first_m);
+  const int in_band = tile_lin % band_size;
+  const int m_tile = first_m + in_band % band_rows;
+  const int n_tile = in_band / band_rows;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lc = lane & 15;
   const int lk = lane >> 4;
-  const int M = a.M, N = a.N;
-  const int G = a.K / kGroup;
-
-  // ---- tile assignment ----
-  const int tiles = a.mtiles * a.ntiles;
-  int tid_lin = blockIdx.x;
-  if ((gridDim.x & 7) == 0) {
-    const int per_xcd = gridDim.x >> 3;
-    tid_lin = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  }
-  if (tid_lin >= tiles) return;
-  const int band_size = kGemmBand * a.ntiles;
-  const int band = tid_lin / band_size;
-  const int first_m = band * kGemmBand;
-  const int band_rows = min(kGemmBand, a.mtiles - first_m);
-  const int in_band = tid_lin % band_size;
-  const int m_tile = first_m + in_band % band_rows;
-  const int n_tile = in_band / band_rows;
+  const int M = L.M, N = P.N;
+  const int G = P.K / kGroup;
+  const int g_begin = split * P.gps;
+  const int g_end = min(G, g_begin + P.gps);
   const int m0 = m_tile * kGemmRows;
-  const int col0 = n_tile * kGemmCols + wave * 64 + lc * 4;
-  const bool vec_w = (a.vec & 1) != 0;
+  const int col0 = n_tile * 4 * WCOLS + wave * WCOLS + lc * CPL;
 
   // ---- operand sources ----
-  const uint32_t ldp = (uint32_t)a.ldp;
-  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.packed, (uint32_t)((size_t)(a.K / 2) * a.ldp));
-  const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.scale, (uint32_t)((size_t)G * a.lds * 4));
+  const uint32_t ldp = (uint32_t)P.ldp;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(P.packed, (uint32_t)((size_t)(P.K / 2) * P.ldp));
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(P.scale, (uint32_t)((size_t)G * P.lds * 4));
   const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
   // Activation rows this lane copies (clamped: rows past M compute values that are never stored).
-  const uint16_t* xlane = a.x + (int64_t)(m0 + lc) * a.ldx + (wave * 4 + lk) * 8;
-  const int64_t xstep = (int64_t)16 * a.ldx;     // 16 rows
+  const uint16_t* xlane = P.x + (int64_t)(m0 + lc) * P.ldx + (wave * 4 + lk) * 8;
+  const int64_t xstep = (int64_t)16 * P.ldx;     // 16 rows
   const int last_full = (M - 1 - m0 - lc) / 16;  // subtiles whose row m0 + 16i + lc < M
   int crow = m0 + (threadIdx.x & 127);
   crow = crow < M ? crow : M - 1;
@@ -762,20 +606,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W4A16_GEMM_
                                        16, 0, 0);
     }
     if (wave < 2)
-      __builtin_amdgcn_global_load_lds((const void*)(a.part + (int64_t)g * M + crow),
+      __builtin_amdgcn_global_load_lds((const void*)(P.rowsum + (int64_t)g * M + crow),
                                        (void __attribute__((address_space(3)))*)&Cs[b][wave * 64], 4, 0, 0);
   };
-  auto load_b = [&](int g, uint32_t (&raw)[4][4], float (&s)[4]) {
+  auto load_b = [&](int g, uint32_t (&raw)[4][4], float (&s)[CPL]) {
     if constexpr (FULL) {
       const uint32_t gbase = (uint32_t)g * kPackedRowsPerGroup * ldp;
 #pragma unroll
       for (int st = 0; st < 4; ++st)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          raw[st][r] = __builtin_amdgcn_raw_buffer_load_b32(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, 0);
-      const f32x4_t v = __builtin_bit_cast(
-          f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, (uint32_t)col0 * 4u, (uint32_t)g * (uint32_t)a.lds * 4u, 0));
-      s[0] = v[0]; s[1] = v[1]; s[2] = v[2]; s[3] = v[3];
+        for (int r = 0; r < 4; ++r) {
+          uint32_t w[1];
+          buffer_load_bytes<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, w);
+          raw[st][r] = w[0];
+        }
+      const uint32_t soff = (uint32_t)g * (uint32_t)P.lds * 4u;
+      if constexpr (CPL == 4) {
+        const f32x4_t v =
+            __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, (uint32_t)col0 * 4u, soff, 0));
+        s[0] = v[0]; s[1] = v[1]; s[2] = v[2]; s[3] = v[3];
+      } else {
+        const f32x2_t v =
+            __builtin_bit_cast(f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(srs, (uint32_t)col0 * 4u, soff, 0));
+        s[0] = v[0]; s[1] = v[1];
+      }
     } else {
 #pragma unroll
       for (int st = 0; st < 4; ++st)
@@ -783,48 +637,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W4A16_GEMM_
         for (int r = 0; r < 4; ++r) {
           const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
           uint32_t w[1];
-          load_packed<4, false>(a.packed + pr * a.ldp, col0, N, vec_w, w);
+          load_packed<CPL, false>(P.packed + pr * P.ldp, col0, N, (P.vec & 1) != 0, w);
           raw[st][r] = w[0];
         }
-      load_scales<4, false>(a.scale + (int64_t)g * a.lds, col0, N, vec_w, s);
+      load_scales<CPL, false>(P.scale + (int64_t)g * P.lds, col0, N, (P.vec & 1) != 0, s);
     }
   };
 
-  f32x4_t U[kGemmMT][4];
+  W4A16_MARK(0);
+  f32x4_t U[kGemmMT][CPL];
 #pragma unroll
   for (int i = 0; i < kGemmMT; ++i)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) U[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < CPL; ++t) U[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   uint32_t raw[4][4];
-  float s[4];
-  float s_ref[4];      // scale U is currently expressed in (per column)
-  load_b(0, raw, s);
-  stage_a(0, 0);
+  float s[CPL];
+  float s_ref[CPL];  // scale U is currently expressed in (per column)
+  load_b(g_begin, raw, s);
+  stage_a(g_begin, 0);
+  W4A16_MARK(1);
 #pragma unroll
-  for (int t = 0; t < 4; ++t) s_ref[t] = clamp_scale(s[t]);
+  for (int t = 0; t < CPL; ++t) s_ref[t] = clamp_scale(s[t]);
 
-  for (int g = 0; g < G; ++g) {
-    const int b = g & 1;
+  for (int g = g_begin; g < g_end; ++g) {
+    const int b = (g - g_begin) & 1;
     // Direct-to-LDS copies of this group (issued one iteration earlier) must
     // have landed before the barrier publishes them.
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    wait_vmem();
     __syncthreads();
 
-    const bool has_next = g + 1 < G;
+    const bool has_next = g + 1 < g_end;
     uint32_t raw_n[4][4];
-    float s_n[4];
+    float s_n[CPL];
     if (has_next) {
       stage_a(g + 1, b ^ 1);
       load_b(g + 1, raw_n, s_n);
     }
 
     // Fold: U <- U * (s_ref / s) - 136 * rowsum.  (U is zero before the first
-    // group, where the ratio is 1.)  s_ref / s uses the hardware reciprocal:
-    // relative error ~1 ulp, the order of the fp32 rounding of the fold.
-    float rho[4];
+    // group, so its ratio only has to be finite.)  s_ref / s uses the hardware
+    // reciprocal: relative error ~1 ulp, the order of the fold's own rounding.
+    float rho[CPL];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < CPL; ++t) {
       const float sc = clamp_scale(s[t]);
       rho[t] = s_ref[t] * __builtin_amdgcn_rcpf(sc);
       s_ref[t] = sc;
@@ -833,26 +689,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W4A16_GEMM_
     for (int i = 0; i < kGemmMT; ++i) {
       const f32x4_t c4 = *reinterpret_cast<const f32x4_t*>(&Cs[b][16 * i + 4 * lk]);
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < CPL; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) U[i][t][r] = __builtin_fmaf(U[i][t][r], rho[t], -c4[r]);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      Prep p[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) p[r] = prep(raw[st][r]);
-      bf16x8_t B[4];
-      B[0] = as_bf16x8(u32x4_t{pair_of<0>(p[0]), pair_of<0>(p[1]), pair_of<0>(p[2]), pair_of<0>(p[3])});
-      B[1] = as_bf16x8(u32x4_t{pair_of<1>(p[0]), pair_of<1>(p[1]), pair_of<1>(p[2]), pair_of<1>(p[3])});
-      B[2] = as_bf16x8(u32x4_t{pair_of<2>(p[0]), pair_of<2>(p[1]), pair_of<2>(p[2]), pair_of<2>(p[3])});
-      B[3] = as_bf16x8(u32x4_t{pair_of<3>(p[0]), pair_of<3>(p[1]), pair_of<3>(p[2]), pair_of<3>(p[3])});
+      bf16x8_t B[CPL];
+      gemm_unpack<CPL>(raw[st], B);
 #pragma unroll
       for (int i = 0; i < kGemmMT; ++i) {
         const bf16x8_t A = __builtin_bit_cast(bf16x8_t, As[b][(st * kGemmMT + i) * 64 + lane]);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) U[i][t] = mfma16(A, B[t], U[i][t]);
+        for (int t = 0; t < CPL; ++t) U[i][t] = mfma16(A, B[t], U[i][t]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -863,38 +713,107 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W4A16_GEMM_
 #pragma unroll
         for (int r = 0; r < 4; ++r) raw[st][r] = raw_n[st][r];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) s[t] = s_n[t];
+      for (int t = 0; t < CPL; ++t) s[t] = s_n[t];
     }
   }
 
-  // ---- store y = U * s_ref: lane holds rows m0 + 16i + 4lk + r, columns col0 .. col0+3 ----
-  const float* outs = s_ref;
-  const bool vec_y = FULL ? (a.vec & 4) != 0 : ((a.vec & 4) != 0 && col0 + 4 <= N);
+  // ---- output: lane holds rows m0 + 16i + 4lk + r, columns col0 .. col0+CPL-1 ----
+  if (P.nsplit == 1) {
+    const bool vec_y = FULL ? (P.vec & 4) != 0 : ((P.vec & 4) != 0 && col0 + CPL <= N);
 #pragma unroll
-  for (int i = 0; i < kGemmMT; ++i)
+    for (int i = 0; i < kGemmMT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 16 * i + 4 * lk + r;
+        if (m >= M) continue;
+        uint16_t* dst = P.y + (int64_t)m * P.ldy + col0;
+        uint16_t h[CPL];
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) h[t] = f32_to_bf16(U[i][t][r] * s_ref[t]);
+        if (vec_y) {
+          if constexpr (CPL == 4)
+            *reinterpret_cast<u32x2_t*>(dst) =
+                u32x2_t{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+          else
+            *reinterpret_cast<uint32_t*>(dst) = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+        } else {
+#pragma unroll
+          for (int t = 0; t < CPL; ++t)
+            if (col0 + t < N) dst[t] = h[t];
+        }
+      }
+    return;
+  }
+
+  W4A16_MARK(3);
+  // ---- K split: store this split's fp32 tile (already scaled); splitk_reduce_kernel
+  // sums the splits in order in the next launch ----
+  float* part = P.part + (size_t)split * M * N;
+#pragma unroll
+  for (int i = 0; i < kGemmMT; ++i) {
+    if (m0 + 16 * i >= M) break;  // wave-uniform: the rest of the tile is past M
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = m0 + 16 * i + 4 * lk + r;
       if (m >= M) continue;
-      uint16_t* dst = a.y + (int64_t)m * a.ldy + col0;
-      const uint16_t h0 = f32_to_bf16(U[i][0][r] * outs[0]);
-      const uint16_t h1 = f32_to_bf16(U[i][1][r] * outs[1]);
-      const uint16_t h2 = f32_to_bf16(U[i][2][r] * outs[2]);
-      const uint16_t h3 = f32_to_bf16(U[i][3][r] * outs[3]);
-      if (vec_y) {
-        *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{(uint32_t)h0 | ((uint32_t)h1 << 16),
-                                                   (uint32_t)h2 | ((uint32_t)h3 << 16)};
+      float* dst = part + (size_t)m * N + col0;
+      float v[CPL];
+#pragma unroll
+      for (int t = 0; t < CPL; ++t) v[t] = U[i][t][r] * s_ref[t];
+      if (FULL) {
+        if constexpr (CPL == 4)
+          *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{v[0], v[1], v[2], v[3]};
+        else
+          *reinterpret_cast<f32x2_t*>(dst) = f32x2_t{v[0], v[1]};
       } else {
-        if (col0 + 0 < N) dst[0] = h0;
-        if (col0 + 1 < N) dst[1] = h1;
-        if (col0 + 2 < N) dst[2] = h2;
-        if (col0 + 3 < N) dst[3] = h3;
+#pragma unroll
+        for (int t = 0; t < CPL; ++t)
+          if (col0 + t < N) dst[t] = v[t];
       }
     }
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Dequantize: out[k, n] = q[k, n] * s[k/128, n] (engine/kernels/quant.py:122-156).
+// Split-K reduction of the GEMM: y = bf16(sum over splits, in split order, of
+// part[split]).  Four consecutive elements of the dense [M, N] partial per
+// thread; grid = sum of red_wgs over the split problems of the launch.
+// ---------------------------------------------------------------------------
+constexpr int kReduceElems = 4 * 256;  // elements per workgroup
+
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(Launch L) {
+  const int wg = blockIdx.x;
+  int pi = 0;
+  for (int i = 1; i < L.count; ++i)
+    if (wg >= L.p[i].red_begin) pi = i;
+  const Problem& P = L.p[pi];
+  const int M = L.M, N = P.N;
+  const int64_t total = (int64_t)M * N;
+  const int64_t e0 = (int64_t)(wg - P.red_begin) * kReduceElems + 4 * threadIdx.x;
+  if (e0 >= total) return;
+  const size_t stride = (size_t)total;
+  if ((N & 3) == 0 && (P.vec & 4)) {
+    // Four elements in one row: 16-byte loads, one 8-byte store.
+    const float* src = P.part + e0;
+    f32x4_t acc = *reinterpret_cast<const f32x4_t*>(src);
+    for (int sp = 1; sp < P.nsplit; ++sp) acc += *reinterpret_cast<const f32x4_t*>(src + sp * stride);
+    const int64_t m = e0 / N, n = e0 % N;
+    *reinterpret_cast<u32x2_t*>(P.y + m * P.ldy + n) =
+        u32x2_t{(uint32_t)f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16),
+                (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16)};
+  } else {
+    for (int j = 0; j < 4; ++j) {
+      const int64_t e = e0 + j;
+      if (e >= total) break;
+      float acc = P.part[e];
+      for (int sp = 1; sp < P.nsplit; ++sp) acc += P.part[e + sp * stride];
+      P.y[(e / N) * P.ldy + e % N] = f32_to_bf16(acc);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dequantize: out[k, n] = q[k, n] * s[k/g, n] (engine/kernels/quant.py:122-156).
 // With a bf16 output the scale is first rounded to bf16, then the product is
 // rounded to bf16, which is what `dequantize_weight_int4(packed, scale.to(bf16))`
 // computes.  One thread per packed byte.
@@ -909,7 +828,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
   const int i = (int)(idx / N);
   const int n = (int)(idx % N);
   const int8_t byte = (int8_t)packed[(int64_t)i * ldp + n];
-  const int q_even = byte >> 4;                          // arithmetic shift: [-8, 7]
+  const int q_even = byte >> 4;  // arithmetic shift: [-8, 7]
   const int q_odd = (int)(int8_t)(uint8_t)(byte << 4) >> 4;
   const int k = 2 * i;
   float s = scale[(int64_t)(k / group_size) * lds + n];
@@ -935,17 +854,11 @@ __global__ __launch_bounds__(256) void zero_kernel(uint16_t* __restrict__ y, int
 // ---------------------------------------------------------------------------
 // Host-side planning.
 // ---------------------------------------------------------------------------
-struct Plan {
-  int kind;    // 0 = skinny, 1 = gemm, 2 = gemv (M <= 16, activations in LDS)
-  size_t lds_bytes;
-  int mt, cpl, waves, pipe;  // skinny variant
-  int strips, nsplit, gps;
-  size_t ws_bytes;
-};
+enum Kind { kGemv = 0, kSkinny = 1, kGemm = 2 };
 
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
-
-bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 int env_int(const char* name, int dflt) {
 #ifdef W4A16_EXP
@@ -956,53 +869,183 @@ int env_int(const char* name, int dflt) {
   return dflt;
 }
 
-Plan make_plan(int M, int N, int K) {
-  Plan p{};
-  const int G = K / kGroup;
-  if (M > 32) {
-    p.kind = 1;
-    p.ws_bytes = (size_t)kCounterBytes + (size_t)G * M * sizeof(float);
-    return p;
+struct Plan {
+  Kind kind;
+  int cpl;
+  bool full;           // every problem takes the unconditional (aligned, full tile) load path
+  size_t lds_bytes;    // dynamic LDS (gemv / skinny)
+  size_t ws_bytes;
+  int total_wgs;
+  int rs_wgs;          // rowsum_kernel workgroups
+  int red_wgs;         // splitk_reduce_kernel workgroups (gemm with split K)
+  bool too_many_counters;
+  Launch L;            // device table (workspace pointers filled in by bind())
+  size_t part_off[kMaxProblems], rowsum_off[kMaxProblems];
+  int counter_off[kMaxProblems];
+  int rowsum_src[kMaxProblems];  // problem whose row sums this one uses
+};
+
+// Validate one problem; returns a W4A16 status.
+int check_problem(const w4a16_problem& q, int M) {
+  if (q.N < 0 || q.K < 0) return W4A16_ERR_SHAPE;
+  if (q.K % kGroup != 0) return W4A16_ERR_K_GROUP;
+  if (M == 0 || q.N == 0) return W4A16_OK;
+  if (!q.y) return W4A16_ERR_NULL;
+  if (q.K > 0 && (!q.x || !q.packed || !q.scale)) return W4A16_ERR_NULL;
+  if (q.ldy < q.N || (q.K > 0 && (q.ldx < q.K || q.ldp < q.N || q.lds < q.N))) return W4A16_ERR_SHAPE;
+  return W4A16_OK;
+}
+
+bool gemm_x_ok(const w4a16_problem& q) { return aligned(q.x, 16) && q.ldx % 8 == 0; }
+
+// Plan a launch over problems that all have M > 0, N > 0, K > 0.
+Plan make_plan(const w4a16_problem* probs, int count, int M) {
+  Plan pl{};
+  pl.L.count = count;
+  pl.L.M = M;
+  pl.kind = M <= 16 ? kGemv : (M <= 32 ? kSkinny : kGemm);
+  bool full = true;
+  for (int i = 0; i < count; ++i) {
+    const w4a16_problem& q = probs[i];
+    Problem& P = pl.L.p[i];
+    P.x = static_cast<const uint16_t*>(q.x);
+    P.ldx = q.ldx;
+    P.packed = reinterpret_cast<const uint8_t*>(q.packed);
+    P.ldp = q.ldp;
+    P.scale = q.scale;
+    P.lds = q.lds;
+    P.y = static_cast<uint16_t*>(q.y);
+    P.ldy = q.ldy;
+    P.N = q.N;
+    P.K = q.K;
+    const bool vw = aligned(q.packed, 16) && q.ldp % 16 == 0 && aligned(q.scale, 16) && q.lds % 4 == 0;
+    const bool vx = aligned(q.x, 16) && q.ldx % 8 == 0;
+    const bool vy = aligned(q.y, 8) && q.ldy % 4 == 0;
+    P.vec = (vw ? 1 : 0) | (vx ? 2 : 0) | (vy ? 4 : 0);
+    P.rs_begin = -1;
+    pl.rowsum_src[i] = i;
   }
-  // GEMV kernel: 4 waves x one 128-row group each per workgroup; activations
-  // of the workgroup's K range staged in LDS.
-  if (M <= 16 && G > 0 && env_int("W4A16_GEMV", 1)) {
-    p.kind = 2;
-    p.cpl = env_int("W4A16_CPL", 8);
-    p.strips = ceil_div(N, 16 * p.cpl);
-    p.gps = env_int("W4A16_GPS", 4);
-    p.nsplit = ceil_div(G, p.gps);
-    p.lds_bytes = (size_t)M * (p.gps * kGroup + 8) * 2;
-    const size_t rbytes = (size_t)4 * M * 16 * p.cpl * 4;
-    if (rbytes > p.lds_bytes) p.lds_bytes = rbytes;
-    p.ws_bytes = p.nsplit > 1 ? (size_t)kCounterBytes + (size_t)p.nsplit * M * N * sizeof(float) : 0;
-    return p;
+
+  int counters = 0;
+  size_t ws = kCounterBytes;
+  if (pl.kind == kGemv || pl.kind == kSkinny) {
+    int cpl = pl.kind == kSkinny ? kSkinnyCPL : env_int("W4A16_CPL", 8);
+    if (pl.kind == kGemv && cpl == 8) {
+      // 64-column strips when a problem is not a multiple of 128 columns.
+      for (int i = 0; i < count; ++i)
+        if (probs[i].N % 128 != 0) cpl = 4;
+    }
+    pl.cpl = cpl;
+    const int wcols = 16 * cpl;
+    int wg = 0;
+    size_t lds = 0;
+    for (int i = 0; i < count; ++i) {
+      Problem& P = pl.L.p[i];
+      const int G = P.K / kGroup;
+      P.tiles_m = 1;
+      P.tiles_n = ceil_div(P.N, wcols);
+      if (pl.kind == kGemv) {
+        P.gps = env_int("W4A16_GPS", 4);
+        P.nsplit = ceil_div(G, P.gps);
+        lds = std::max(lds, (size_t)M * (P.gps * kGroup + 8) * 2);
+        lds = std::max(lds, (size_t)4 * M * wcols * 4);
+      } else {
+        // Split K until ~2 workgroups per CU, keeping at least one group per
+        // wave and the fp32 partial traffic within a quarter of the weights.
+        int nsplit = ceil_div(512, P.tiles_n);
+        const int by_traffic = std::max(1, (int)((int64_t)P.K / (64 * (int64_t)M)));
+        nsplit = std::min(nsplit, std::min(by_traffic, ceil_div(G, 4)));
+        nsplit = std::max(1, nsplit);
+        P.gps = ceil_div(G, nsplit);
+        P.nsplit = ceil_div(G, P.gps);
+        lds = std::max(lds, (size_t)4 * M * wcols * 4);
+      }
+      P.wg_begin = wg;
+      wg += P.tiles_n * P.nsplit;
+      const size_t wbytes = (size_t)(P.K / 2) * P.ldp, sbytes = (size_t)G * P.lds * 4;
+      full = full && (P.vec & 1) && P.N % wcols == 0 && wbytes < 0xffffffffull && sbytes < 0xffffffffull;
+      if (P.nsplit > 1) {
+        pl.counter_off[i] = counters;
+        counters += P.tiles_n;
+        pl.part_off[i] = ws;
+        ws = align256(ws + (size_t)P.nsplit * M * P.N * 4);
+      }
+    }
+    pl.lds_bytes = lds;
+    pl.total_wgs = wg;
+  } else {
+    // GEMM: 256-column tiles unless that leaves the chip under-filled.
+    int t4 = 0;
+    for (int i = 0; i < count; ++i) t4 += ceil_div(M, kGemmRows) * ceil_div(probs[i].N, 256);
+    pl.cpl = env_int("W4A16_GCPL", t4 < 384 ? 2 : 4);
+    const int tcols = 64 * pl.cpl;
+    int tiles_total = 0;
+    for (int i = 0; i < count; ++i) tiles_total += ceil_div(M, kGemmRows) * ceil_div(probs[i].N, tcols);
+    int wg = 0;
+    for (int i = 0; i < count; ++i) {
+      Problem& P = pl.L.p[i];
+      const int G = P.K / kGroup;
+      P.tiles_m = ceil_div(M, kGemmRows);
+      P.tiles_n = ceil_div(P.N, tcols);
+      const int tiles = P.tiles_m * P.tiles_n;
+      // Split K when the launch has fewer than ~1.5 workgroups per CU slot,
+      // keeping >= 4 groups per split.
+      int nsplit = tiles_total >= 384 ? 1 : std::max(1, 512 / tiles_total);
+      nsplit = std::min(nsplit, std::max(1, G / 4));
+      nsplit = env_int("W4A16_GSPLIT", nsplit);
+      if (pl.cpl == 4) nsplit = 1;  // 256-column tiles only when the chip is already full
+      while (nsplit > 1 && (size_t)nsplit * M * P.N * 4 >= 0xffffffffull) --nsplit;  // 32-bit buffer offsets
+      P.gps = ceil_div(G, nsplit);
+      P.nsplit = ceil_div(G, P.gps);
+      P.wg_begin = wg;
+      wg += tiles * P.nsplit;
+      const size_t wbytes = (size_t)(P.K / 2) * P.ldp, sbytes = (size_t)G * P.lds * 4;
+      full = full && aligned(P.packed, pl.cpl) && P.ldp % pl.cpl == 0 && aligned(P.scale, 4 * pl.cpl) &&
+             P.lds % pl.cpl == 0 && P.N % tcols == 0 && wbytes < 0xffffffffull && sbytes < 0xffffffffull;
+      // Row sums, shared by problems with the same activations.
+      for (int j = 0; j < i; ++j)
+        if (probs[j].x == probs[i].x && probs[j].ldx == probs[i].ldx && probs[j].K == probs[i].K &&
+            pl.rowsum_src[j] == j) {
+          pl.rowsum_src[i] = j;
+          break;
+        }
+      if (pl.rowsum_src[i] == i) {
+        pl.rowsum_off[i] = ws;
+        ws = align256(ws + (size_t)G * M * 4);
+        P.rs_begin = pl.rs_wgs;
+        pl.rs_wgs += ceil_div((int64_t)M * G, 16);
+      }
+      P.red_begin = pl.red_wgs;
+      if (P.nsplit > 1) {
+        pl.part_off[i] = ws;
+        ws = align256(ws + (size_t)P.nsplit * M * P.N * 4);
+        pl.red_wgs += ceil_div((int64_t)M * P.N, kReduceElems);
+      }
+    }
+    pl.total_wgs = wg;
   }
-  p.kind = 0;
-  p.mt = M <= 16 ? 1 : 2;
-  p.cpl = env_int("W4A16_CPL", 8);
-  if (p.mt == 2 && p.cpl == 16) p.cpl = 8;
-  const int R = M < 16 * p.mt ? M : 16 * p.mt;
-  // Waves per workgroup: as many as the LDS reduction buffer allows (<= 64 KB).
-  int waves = 16;
-  while (waves > 4 && (size_t)waves * R * 16 * p.cpl * 4 > 65536) waves >>= 1;
-  p.waves = env_int("W4A16_WAVES", waves);
-  p.pipe = env_int("W4A16_PIPE", 0);
-  p.strips = ceil_div(N, 16 * p.cpl);
-  // Split K across workgroups until ~16 waves per CU are resident, keeping at
-  // least one group per wave and the fp32 partial traffic (write + read) within
-  // a quarter of the weight bytes.
-  int nsplit = ceil_div(256 * 16, (int64_t)p.strips * p.waves);
-  const int by_traffic = (int)((int64_t)K / (64 * (int64_t)M));
-  if (nsplit > by_traffic) nsplit = by_traffic;
-  const int max_split = ceil_div(G, p.waves);
-  if (nsplit > max_split) nsplit = max_split;
-  if (nsplit < 1) nsplit = 1;
-  nsplit = env_int("W4A16_NSPLIT", nsplit);
-  p.gps = G > 0 ? ceil_div(G, nsplit) : 0;
-  p.nsplit = G > 0 ? ceil_div(G, p.gps) : 1;
-  p.ws_bytes = p.nsplit > 1 ? (size_t)kCounterBytes + (size_t)p.nsplit * M * N * sizeof(float) : 0;
-  return p;
+  pl.full = full;
+  pl.L.total_wgs = pl.total_wgs;
+  pl.too_many_counters = counters > kMaxCounters;
+  pl.ws_bytes = (counters > 0 || pl.kind == kGemm) ? ws : 0;
+  return pl;
+}
+
+// Point the device table at the workspace.
+void bind(Plan& pl, void* workspace) {
+  char* ws = static_cast<char*>(workspace);
+  for (int i = 0; i < pl.L.count; ++i) {
+    Problem& P = pl.L.p[i];
+    if (P.nsplit > 1) {
+      if (pl.kind != kGemm) P.counters = reinterpret_cast<uint32_t*>(ws) + pl.counter_off[i];
+      P.part = reinterpret_cast<float*>(ws + pl.part_off[i]);
+    }
+    if (pl.kind == kGemm) P.rowsum = reinterpret_cast<float*>(ws + pl.rowsum_off[pl.rowsum_src[i]]);
+  }
+#ifdef W4A16_EXP
+  pl.L.trace = getenv("W4A16_TRACE") ? reinterpret_cast<uint64_t*>(strtoull(getenv("W4A16_TRACE"), nullptr, 0))
+                                     : nullptr;
+#endif
 }
 
 int launch_status() {
@@ -1011,50 +1054,127 @@ int launch_status() {
 }
 
 template <int CPL>
-int launch_gemv_c(const LinearArgs& a, const Plan& p, hipStream_t stream) {
-  // Buffer loads address at most 4 GiB per resource.
-  const bool full = (a.vec & 1) && (a.N % (16 * CPL) == 0) && (size_t)(a.K / 2) * a.ldp < 0xffffffffull &&
-                    (size_t)(a.K / kGroup) * a.lds * 4 < 0xffffffffull;
-  if (full)
-    hipLaunchKernelGGL((gemv_kernel<CPL, true>), dim3(p.strips, p.nsplit), dim3(256), p.lds_bytes, stream, a);
+int launch_gemv(const Plan& pl, hipStream_t s) {
+  if (pl.full)
+    hipLaunchKernelGGL((gemv_kernel<CPL, true>), dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
   else
-    hipLaunchKernelGGL((gemv_kernel<CPL, false>), dim3(p.strips, p.nsplit), dim3(256), p.lds_bytes, stream, a);
+    hipLaunchKernelGGL((gemv_kernel<CPL, false>), dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
   return launch_status();
 }
 
-int launch_gemv(const LinearArgs& a, const Plan& p, hipStream_t stream) {
-  if (p.cpl == 4) return launch_gemv_c<4>(a, p, stream);
-  if (p.cpl == 16) return launch_gemv_c<16>(a, p, stream);
-  return launch_gemv_c<8>(a, p, stream);
-}
-
-template <int MT, int CPL, int WAVES, bool PIPE>
-int launch_skinny_p(const LinearArgs& a, const Plan& p, hipStream_t stream) {
-  const int R = a.M < 16 * MT ? a.M : 16 * MT;
-  const size_t shmem = (size_t)WAVES * R * 16 * CPL * sizeof(float);
-  const bool full = (a.vec & 1) && (a.N % (16 * CPL) == 0);
-  if (full)
-    hipLaunchKernelGGL((skinny_kernel<MT, CPL, WAVES, true, PIPE>), dim3(p.strips, p.nsplit), dim3(WAVES * 64),
-                       shmem, stream, a);
+template <int CPL>
+int launch_gemm(const Plan& pl, hipStream_t s) {
+  const int grid = (pl.total_wgs + 7) & ~7;
+  if (pl.full)
+    hipLaunchKernelGGL((gemm_kernel<CPL, true>), dim3(grid), dim3(256), 0, s, pl.L);
   else
-    hipLaunchKernelGGL((skinny_kernel<MT, CPL, WAVES, false, PIPE>), dim3(p.strips, p.nsplit), dim3(WAVES * 64),
-                       shmem, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<CPL, false>), dim3(grid), dim3(256), 0, s, pl.L);
   return launch_status();
 }
 
-template <int MT, int CPL, int WAVES>
-int launch_skinny_w(const LinearArgs& a, const Plan& p, hipStream_t stream) {
-  if (p.pipe) return launch_skinny_p<MT, CPL, WAVES, true>(a, p, stream);
-  return launch_skinny_p<MT, CPL, WAVES, false>(a, p, stream);
-}
+// Problems that run() launches separately: empty, K == 0, or (M > 32) with
+// activations the GEMM cannot stage with 16-byte copies.
+bool separate(const w4a16_problem& q, int M) { return M == 0 || q.N == 0 || q.K == 0 || (M > 32 && !gemm_x_ok(q)); }
 
-template <int MT, int CPL>
-int launch_skinny(const LinearArgs& a, const Plan& p, hipStream_t stream) {
-  switch (p.waves) {
-    case 16: return launch_skinny_w<MT, CPL, 16>(a, p, stream);
-    case 8: return launch_skinny_w<MT, CPL, 8>(a, p, stream);
-    default: return launch_skinny_w<MT, CPL, 4>(a, p, stream);
+int run(const w4a16_problem* probs, int count, int M, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  w4a16_problem live[kMaxProblems];
+  int n = 0;
+  for (int i = 0; i < count; ++i) {
+    const w4a16_problem& q = probs[i];
+    if (M == 0 || q.N == 0) continue;
+    if (q.K == 0) {
+      hipLaunchKernelGGL(zero_kernel, dim3(ceil_div((int64_t)M * q.N, 256)), dim3(256), 0, s,
+                         static_cast<uint16_t*>(q.y), q.ldy, M, q.N);
+      const int rc = launch_status();
+      if (rc != W4A16_OK) return rc;
+      continue;
+    }
+    if (separate(q, M)) {
+      // Unaligned activations with M > 32: 32 rows at a time through the skinny kernel.
+      for (int m0 = 0; m0 < M; m0 += 32) {
+        w4a16_problem c = q;
+        c.x = static_cast<const uint16_t*>(q.x) + (int64_t)m0 * q.ldx;
+        c.y = static_cast<uint16_t*>(q.y) + (int64_t)m0 * q.ldy;
+        const int rc = run(&c, 1, M - m0 < 32 ? M - m0 : 32, workspace, workspace_bytes, s);
+        if (rc != W4A16_OK) return rc;
+      }
+      continue;
+    }
+    live[n++] = q;
   }
+  if (n == 0) return W4A16_OK;
+  if (M > 16 && M <= 32 && n > 1) {
+    // The skinny kernel takes one problem per launch.
+    for (int i = 0; i < n; ++i) {
+      const int rc = run(&live[i], 1, M, workspace, workspace_bytes, s);
+      if (rc != W4A16_OK) return rc;
+    }
+    return W4A16_OK;
+  }
+  Plan pl = make_plan(live, n, M);
+  if (pl.too_many_counters) return W4A16_ERR_TOO_LARGE;
+  if (pl.ws_bytes > 0 && (!workspace || workspace_bytes < pl.ws_bytes)) return W4A16_ERR_WORKSPACE;
+  bind(pl, workspace);
+  if (pl.kind == kGemv) return pl.cpl == 4 ? launch_gemv<4>(pl, s) : launch_gemv<8>(pl, s);
+  if (pl.kind == kSkinny) {
+    if (pl.full)
+      hipLaunchKernelGGL(skinny_kernel<true>, dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
+    else
+      hipLaunchKernelGGL(skinny_kernel<false>, dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
+    return launch_status();
+  }
+  hipLaunchKernelGGL(rowsum_kernel, dim3(pl.rs_wgs), dim3(256), 0, s, pl.L);
+  const int rc = launch_status();
+  if (rc != W4A16_OK) return rc;
+  const int rc2 = pl.cpl == 2 ? launch_gemm<2>(pl, s) : launch_gemm<4>(pl, s);
+  if (rc2 != W4A16_OK || pl.red_wgs == 0) return rc2;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(pl.red_wgs), dim3(256), 0, s, pl.L);
+  return launch_status();
+}
+
+// Workspace run() needs for these problems (0 when none).
+int workspace_for(const w4a16_problem* probs, int count, int M, size_t* bytes) {
+  *bytes = 0;
+  w4a16_problem live[kMaxProblems];
+  int n = 0;
+  for (int i = 0; i < count; ++i) {
+    const w4a16_problem& q = probs[i];
+    if (M == 0 || q.N == 0 || q.K == 0) continue;
+    if (separate(q, M)) {
+      size_t b = 0;
+      const int rc = workspace_for(&q, 1, 32, &b);
+      if (rc != W4A16_OK) return rc;
+      *bytes = std::max(*bytes, b);
+      continue;
+    }
+    live[n++] = q;
+  }
+  if (n == 0) return W4A16_OK;
+  if (M > 16 && M <= 32 && n > 1) {
+    for (int i = 0; i < n; ++i) {
+      size_t b = 0;
+      const int rc = workspace_for(&live[i], 1, M, &b);
+      if (rc != W4A16_OK) return rc;
+      *bytes = std::max(*bytes, b);
+    }
+    return W4A16_OK;
+  }
+  const Plan pl = make_plan(live, n, M);
+  if (pl.too_many_counters) return W4A16_ERR_TOO_LARGE;
+  *bytes = std::max(*bytes, pl.ws_bytes);
+  return W4A16_OK;
+}
+
+int check_all(const w4a16_problem* probs, int count, int M, int group_size) {
+  if (count < 0 || count > kMaxProblems) return W4A16_ERR_SHAPE;
+  if (count > 0 && !probs) return W4A16_ERR_NULL;
+  if (M < 0) return W4A16_ERR_SHAPE;
+  if (group_size != kGroup) return W4A16_ERR_GROUP_SIZE;
+  for (int i = 0; i < count; ++i) {
+    const int rc = check_problem(probs[i], M);
+    if (rc != W4A16_OK) return rc;
+  }
+  return W4A16_OK;
 }
 
 }  // namespace
@@ -1070,7 +1190,8 @@ const char* w4a16_error_string(int code) {
   switch (code) {
     case W4A16_OK: return "ok";
     case W4A16_ERR_NULL: return "null pointer argument";
-    case W4A16_ERR_SHAPE: return "invalid shape (negative size or leading dimension smaller than the row)";
+    case W4A16_ERR_SHAPE:
+      return "invalid shape (negative size, leading dimension smaller than the row, or bad problem count)";
     case W4A16_ERR_K_GROUP: return "K must be a multiple of group_size (and even) for int4 packing";
     case W4A16_ERR_GROUP_SIZE: return "fused INT4 kernel requires group_size=128";
     case W4A16_ERR_WORKSPACE: return "workspace missing or smaller than w4a16_workspace_size()";
@@ -1087,94 +1208,34 @@ int w4a16_workspace_size(int M, int N, int K, int group_size, size_t* bytes) {
   if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
   if (group_size != kGroup) return W4A16_ERR_GROUP_SIZE;
   if (K % kGroup != 0) return W4A16_ERR_K_GROUP;
-  if (M == 0 || N == 0) return W4A16_OK;
-  const Plan p = make_plan(M, N, K);
-  *bytes = p.ws_bytes;
-  return W4A16_OK;
+  // Sized for contiguous, 256-byte aligned operands (what the wrapper passes).
+  const uintptr_t a = 256;
+  const w4a16_problem q{reinterpret_cast<const void*>(a), K, reinterpret_cast<const int8_t*>(a), N,
+                        reinterpret_cast<const float*>(a), N, reinterpret_cast<void*>(a), N, N, K};
+  return workspace_for(&q, 1, M, bytes);
 }
 
-int w4a16_linear(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, const float* scale,
-                 int64_t lds, void* y, int64_t ldy, int M, int N, int K, int group_size, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int M, int group_size, size_t* bytes) {
+  if (!bytes) return W4A16_ERR_NULL;
+  *bytes = 0;
+  const int rc = check_all(problems, count, M, group_size);
+  if (rc != W4A16_OK) return rc;
+  return workspace_for(problems, count, M, bytes);
+}
+
+int w4a16_linear_grouped(const w4a16_problem* problems, int count, int M, int group_size, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  const int rc = check_all(problems, count, M, group_size);
+  if (rc != W4A16_OK) return rc;
+  return run(problems, count, M, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int w4a16_linear(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, const float* scale, int64_t lds,
+                 void* y, int64_t ldy, int M, int N, int K, int group_size, void* workspace, size_t workspace_bytes,
+                 void* stream) {
   if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
-  if (group_size != kGroup) return W4A16_ERR_GROUP_SIZE;
-  if (K % kGroup != 0) return W4A16_ERR_K_GROUP;
-  if (M == 0 || N == 0) return W4A16_OK;
-  if (!y) return W4A16_ERR_NULL;
-  if (K > 0 && (!x || !packed || !scale)) return W4A16_ERR_NULL;
-  if (ldy < N || (K > 0 && (ldx < K || ldp < N || lds < N))) return W4A16_ERR_SHAPE;
-
-  const Plan p = make_plan(M, N, K);
-  if (p.ws_bytes > 0 && (!workspace || workspace_bytes < p.ws_bytes)) return W4A16_ERR_WORKSPACE;
-  if (p.kind != 1 && p.nsplit > 1 && p.strips > kMaxStrips) return W4A16_ERR_TOO_LARGE;
-
-  LinearArgs a{};
-  a.x = static_cast<const uint16_t*>(x);
-  a.ldx = ldx;
-  a.packed = reinterpret_cast<const uint8_t*>(packed);
-  a.ldp = ldp;
-  a.scale = scale;
-  a.lds = lds;
-  a.y = static_cast<uint16_t*>(y);
-  a.ldy = ldy;
-  a.M = M;
-  a.N = N;
-  a.K = K;
-  const bool vw = aligned16(packed) && (ldp % 16 == 0) && aligned16(scale) && (lds % 4 == 0);
-  const bool vx = aligned16(x) && (ldx % 8 == 0);
-  const bool vy = (((uintptr_t)y & 7u) == 0) && (ldy % 4 == 0);
-  a.vec = (vw ? 1 : 0) | (vx ? 2 : 0) | (vy ? 4 : 0);
-#ifdef W4A16_EXP
-  a.trace = getenv("W4A16_TRACE") ? reinterpret_cast<uint64_t*>(strtoull(getenv("W4A16_TRACE"), nullptr, 0)) : nullptr;
-#endif
-  hipStream_t s = static_cast<hipStream_t>(stream);
-
-  if (K == 0) {
-    hipLaunchKernelGGL(zero_kernel, dim3(ceil_div((int64_t)M * N, 256)), dim3(256), 0, s, a.y, ldy, M, N);
-    return launch_status();
-  }
-
-  if (p.kind == 1) {
-    if (!vx) {
-      // The gemm stages activations with 16-byte loads; unaligned activations
-      // are processed 32 rows at a time by the skinny kernel instead.
-      for (int m0 = 0; m0 < M; m0 += 32) {
-        const int mc = M - m0 < 32 ? M - m0 : 32;
-        int rc = w4a16_linear(static_cast<const uint16_t*>(x) + (int64_t)m0 * ldx, ldx, packed, ldp, scale, lds,
-                              static_cast<uint16_t*>(y) + (int64_t)m0 * ldy, ldy, mc, N, K, group_size,
-                              workspace, workspace_bytes, stream);
-        if (rc != W4A16_OK) return rc;
-      }
-      return W4A16_OK;
-    }
-    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-    a.mtiles = ceil_div(M, kGemmRows);
-    a.ntiles = ceil_div(N, kGemmCols);
-    const int64_t items = (int64_t)M * (K / kGroup);
-    hipLaunchKernelGGL(rowsum_kernel, dim3(ceil_div(items, 16)), dim3(256), 0, s, a.x, ldx, M, K, 1, a.part);
-    int rc = launch_status();
-    if (rc != W4A16_OK) return rc;
-    int blocks = a.mtiles * a.ntiles;
-    blocks = (blocks + 7) & ~7;
-    if ((a.vec & 1) && N % kGemmCols == 0)
-      hipLaunchKernelGGL(gemm_kernel<true>, dim3(blocks), dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL(gemm_kernel<false>, dim3(blocks), dim3(256), 0, s, a);
-    return launch_status();
-  }
-
-  a.gps = p.gps;
-  a.nsplit = p.nsplit;
-  if (p.nsplit > 1) {
-    a.counters = static_cast<uint32_t*>(workspace);
-    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-  }
-  if (p.kind == 2) return launch_gemv(a, p, s);
-  if (p.mt == 1 && p.cpl == 16) return launch_skinny<1, 16>(a, p, s);
-  if (p.mt == 1 && p.cpl == 4) return launch_skinny<1, 4>(a, p, s);
-  if (p.mt == 1) return launch_skinny<1, 8>(a, p, s);
-  if (p.cpl == 4) return launch_skinny<2, 4>(a, p, s);
-  return launch_skinny<2, 8>(a, p, s);
+  const w4a16_problem q{x, ldx, packed, ldp, scale, lds, y, ldy, N, K};
+  return w4a16_linear_grouped(&q, 1, M, group_size, workspace, workspace_bytes, stream);
 }
 
 int w4a16_dequant(const int8_t* packed, int64_t ldp, const float* scale, int64_t lds, void* out, int64_t ldo,

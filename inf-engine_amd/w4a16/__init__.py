@@ -7,12 +7,13 @@ in hand-written gfx950 HIP kernels behind the C ABI of include/w4a16.h.
 """
 
 from .layers import linear
-from .quant import dequantize_weight_int4, int4_matmul, quantize_weight_int4
+from .quant import dequantize_weight_int4, int4_matmul, int4_matmul_grouped, quantize_weight_int4
 from .quantize import QuantizedLlamaWeights, _Int4Weight, quantize_llama, quantized_to_device
 
 __all__ = [
     "linear",
     "int4_matmul",
+    "int4_matmul_grouped",
     "quantize_weight_int4",
     "dequantize_weight_int4",
     "quantize_llama",

@@ -29,14 +29,30 @@ W4A16_ERR_TOO_LARGE = 8
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
+MAX_PROBLEMS = 8  # W4A16_MAX_PROBLEMS
+
 # Every symbol include/w4a16.h declares.
 EXPORTED_SYMBOLS = (
     "w4a16_abi_version",
     "w4a16_error_string",
     "w4a16_workspace_size",
     "w4a16_linear",
+    "w4a16_linear_grouped",
+    "w4a16_workspace_size_grouped",
     "w4a16_dequant",
 )
+
+
+class Problem(ctypes.Structure):
+    """struct w4a16_problem of include/w4a16.h."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p), ("ldx", ctypes.c_int64),
+        ("packed", ctypes.c_void_p), ("ldp", ctypes.c_int64),
+        ("scale", ctypes.c_void_p), ("lds", ctypes.c_int64),
+        ("y", ctypes.c_void_p), ("ldy", ctypes.c_int64),
+        ("N", ctypes.c_int), ("K", ctypes.c_int),
+    ]
 
 _lib = None
 _lib_lock = threading.Lock()
@@ -71,6 +87,11 @@ def load_library() -> ctypes.CDLL:
         lib.w4a16_linear.restype = i32
         lib.w4a16_dequant.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
         lib.w4a16_dequant.restype = i32
+        pp = ctypes.POINTER(Problem)
+        lib.w4a16_linear_grouped.argtypes = [pp, i32, i32, i32, vp, sz, vp]
+        lib.w4a16_linear_grouped.restype = i32
+        lib.w4a16_workspace_size_grouped.argtypes = [pp, i32, i32, i32, ctypes.POINTER(sz)]
+        lib.w4a16_workspace_size_grouped.restype = i32
         _lib = lib
         return lib
 
@@ -153,6 +174,40 @@ def linear(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_siz
     )
     check(rc, "w4a16_linear")
     return y
+
+
+def linear_grouped(xs, weights, group_size: int) -> list[torch.Tensor]:
+    """Several projections in one launch; xs[i] is [M, K_i] bf16, weights[i] = (packed, scale)."""
+    lib = load_library()
+    if not 0 < len(weights) <= MAX_PROBLEMS:
+        raise ValueError(f"a grouped call takes 1..{MAX_PROBLEMS} projections, got {len(weights)}")
+    m = xs[0].shape[0]
+    table = (Problem * len(weights))()
+    outs, keep = [], []
+    for i, (x, (packed, scale)) in enumerate(zip(xs, weights)):
+        if x.stride(1) != 1:
+            x = x.contiguous()
+        if packed.stride(1) != 1:
+            packed = packed.contiguous()
+        if scale.stride(1) != 1:
+            scale = scale.contiguous()
+        keep += [x, packed, scale]
+        n = packed.shape[1]
+        y = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+        outs.append(y)
+        table[i] = Problem(x.data_ptr(), x.stride(0), packed.data_ptr(), packed.stride(0), scale.data_ptr(),
+                           scale.stride(0), y.data_ptr(), y.stride(0), n, x.shape[1])
+    dev = xs[0].device
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    nbytes = ctypes.c_size_t(0)
+    check(lib.w4a16_workspace_size_grouped(table, len(weights), m, group_size, ctypes.byref(nbytes)),
+          "w4a16_workspace_size_grouped")
+    ws = get_workspace(dev, stream, nbytes.value)
+    rc = lib.w4a16_linear_grouped(table, len(weights), m, group_size,
+                                  ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+                                  stream)
+    check(rc, "w4a16_linear_grouped")
+    return outs
 
 
 def dequant(packed: torch.Tensor, scale: torch.Tensor, group_size: int, out_dtype: torch.dtype) -> torch.Tensor:

@@ -94,22 +94,8 @@ def dequantize_weight_int4(packed: torch.Tensor, scale: torch.Tensor, group_size
         return _native.dequant(packed, scale.float(), group_size, scale.dtype)
 
 
-def int4_matmul(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_size: int = 128) -> torch.Tensor:
-    """Fused W4A16 matmul ``a @ dequantize(packed, scale)`` without a dense weight.
-
-    Drop-in for engine/kernels/quant.py:243-281.  ``a`` is ``(M, K)`` bf16 on a
-    HIP device, ``packed`` ``(K/2, N)`` int8, ``scale`` ``(K/128, N)`` float32.
-    Returns ``(M, N)`` bf16, allocated on the caller's stream; the call
-    enqueues on the current stream and never synchronises, so it can be
-    captured in a HIP graph once its workspace exists.
-
-    M <= 32 runs the HBM-bound skinny kernel, larger M the MFMA GEMM.
-
-    Raises:
-        AssertionError: ``group_size != 128`` (as engine/kernels/quant.py:267).
-        ValueError: inconsistent shapes.
-        TypeError: host tensors or non-bf16 activations.
-    """
+def _check_operands(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_size: int) -> torch.Tensor:
+    """Shape / dtype / device checks shared by int4_matmul and int4_matmul_grouped; returns fp32 scale."""
     if not a.is_cuda:
         raise TypeError(
             "w4a16.int4_matmul runs only on HIP device tensors; this package has no host "
@@ -132,7 +118,46 @@ def int4_matmul(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, grou
         raise TypeError(f"packed weights must be int8, got {packed.dtype}")
     if packed.device != a.device or scale.device != a.device:
         raise ValueError("a, packed and scale must be on the same device")
-    if scale.dtype != torch.float32:
-        scale = scale.float()
+    return scale if scale.dtype == torch.float32 else scale.float()
+
+
+def int4_matmul_grouped(a, weights, group_size: int = 128) -> list[torch.Tensor]:
+    """Several INT4 projections in one kernel launch: ``[a_i @ dequantize(packed_i, scale_i)]``.
+
+    ``a`` is one ``(M, K)`` bf16 tensor shared by every projection (q/k/v or
+    gate/up of a block) or a list of per-projection activations with a common
+    M (a set of MoE experts).  ``weights`` is a list of ``(packed, scale)``
+    pairs, at most 8.  Results equal ``int4_matmul`` on each pair up to fp32
+    summation order.  No reference counterpart: the reference calls
+    ``int4_matmul`` once per projection (engine/llama_attention.py:83-85,
+    engine/llama_mlp.py:30-33).
+    """
+    xs = list(a) if isinstance(a, (list, tuple)) else [a] * len(weights)
+    if len(xs) != len(weights):
+        raise ValueError("need one activation tensor per weight (or a single shared one)")
+    if len({x.shape[0] for x in xs}) != 1:
+        raise ValueError("all projections of a grouped call must share M")
+    prepared = [(packed, _check_operands(x, packed, scale, group_size)) for x, (packed, scale) in zip(xs, weights)]
+    with torch.cuda.device(xs[0].device):
+        return _native.linear_grouped(xs, prepared, group_size)
+
+
+def int4_matmul(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """Fused W4A16 matmul ``a @ dequantize(packed, scale)`` without a dense weight.
+
+    Drop-in for engine/kernels/quant.py:243-281.  ``a`` is ``(M, K)`` bf16 on a
+    HIP device, ``packed`` ``(K/2, N)`` int8, ``scale`` ``(K/128, N)`` float32.
+    Returns ``(M, N)`` bf16, allocated on the caller's stream; the call
+    enqueues on the current stream and never synchronises, so it can be
+    captured in a HIP graph once its workspace exists.
+
+    M <= 32 runs the HBM-bound decode kernels, larger M the MFMA GEMM.
+
+    Raises:
+        AssertionError: ``group_size != 128`` (as engine/kernels/quant.py:267).
+        ValueError: inconsistent shapes.
+        TypeError: host tensors or non-bf16 activations.
+    """
+    scale = _check_operands(a, packed, scale, group_size)
     with torch.cuda.device(a.device):
         return _native.linear(a, packed, scale, group_size)

@@ -235,6 +235,62 @@ def test_split_k_deterministic_and_counters_reset():
             assert torch.equal(int4_matmul(*p), y0)
 
 
+@pytest.mark.parametrize("m", [1, 5, 16, 24, 40, 300])
+def test_grouped_shared_activations(m):
+    """q/k/v-style group (one x, three weights, ragged N) in one launch."""
+    from w4a16 import int4_matmul, int4_matmul_grouped, synth
+
+    say(f"grouped shared-x m={m}")
+    k = 1024
+    weights = [synth.make_weight(k, n, seed=300 + n) for n in (1024, 256, 320)]
+    x = synth.make_activations(m, k, seed=7 + m)
+    outs = int4_matmul_grouped(x.to(DEV), [(p.to(DEV), s.to(DEV)) for p, s in weights])
+    for (p, s), y in zip(weights, outs):
+        assert y.shape == (m, p.shape[1])
+        check_tolerance(y, orc.fused_reference(x.float().numpy(), p.numpy(), s.numpy()), f"grouped N={p.shape[1]}")
+        if m <= 16:  # decode path: identical arithmetic per problem, so identical bits
+            assert torch.equal(y, int4_matmul(x.to(DEV), p.to(DEV), s.to(DEV)))
+
+
+@pytest.mark.parametrize("m", [1, 8, 24, 96])
+def test_grouped_distinct_activations(m):
+    """MoE-style group: each problem has its own activations and K."""
+    from w4a16 import int4_matmul_grouped, synth
+
+    say(f"grouped distinct-x m={m}")
+    specs = [(512, 768), (1024, 256), (256, 512), (768, 1024)]
+    weights = [synth.make_weight(k, n, seed=k + n) for k, n in specs]
+    xs = [synth.make_activations(m, k, seed=k + m) for k, _ in specs]
+    outs = int4_matmul_grouped([x.to(DEV) for x in xs], [(p.to(DEV), s.to(DEV)) for p, s in weights])
+    for x, (p, s), y in zip(xs, weights, outs):
+        check_tolerance(y, orc.fused_reference(x.float().numpy(), p.numpy(), s.numpy()), f"moe K={x.shape[1]}")
+
+
+@pytest.mark.parametrize("m", [1, 20, 64])
+def test_zero_subnormal_and_extreme_scales(m):
+    """Zero / subnormal scale groups contribute nothing (exactly on the decode
+    path, < 1e-20 per unit on the GEMM path); large scale ratios between groups."""
+    from w4a16 import int4_matmul
+
+    say(f"scales m={m}")
+    k, n = 1024, 512
+    g = torch.Generator().manual_seed(m)
+    packed = torch.randint(-128, 128, (k // 2, n), generator=g, dtype=torch.int8)
+    scale = torch.rand(k // 128, n, generator=g) * 0.01 + 1e-3
+    scale[1, :64] = 0.0                          # zero groups
+    scale[:, 64:70] = 0.0                        # all-zero columns
+    scale[2, 100:140] = 1e-39                    # subnormal
+    scale[3, 200:240] = 1e4                      # large jumps between groups
+    scale[5, 200:240] = 1e-6
+    scale[6, 300:330] = -0.02                    # negative scales
+    x = torch.randn(m, k, generator=g).bfloat16()
+    y = int4_matmul(x.to(DEV), packed.to(DEV), scale.to(DEV))
+    ref = orc.fused_reference(x.float().numpy(), packed.numpy(), scale.numpy())
+    check_tolerance(y, ref, f"scales M={m}")
+    yc = y.float().cpu().numpy()
+    assert np.all(np.abs(yc[:, 64:70]) <= 1e-15)
+
+
 def test_quantize_llama_on_device_matches_dense():
     """quantize_llama -> quantized_to_device -> linear: matches dequantize-then-matmul."""
     from w4a16 import linear, quantize_llama, quantized_to_device
@@ -262,18 +318,24 @@ def test_graph_capture_replays_match_eager():
     and synchronisation, must reproduce the eager result bit for bit."""
     from w4a16 import int4_matmul
 
+    from w4a16 import int4_matmul_grouped
+
     cases = [rand_problem(m, k, n, seed=50 + m) for (m, k, n) in [(1, 4096, 12288), (8, 4096, 1024), (64, 1024, 2048)]]
-    eager = [int4_matmul(*c) for c in cases]
+    xg, pg, sg = rand_problem(1, 4096, 1024, seed=99)
+    _, pg2, sg2 = rand_problem(1, 4096, 3072, seed=98)
+    eager = [int4_matmul(*c) for c in cases] + int4_matmul_grouped(xg, [(pg, sg), (pg2, sg2)])
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
+    def body():
+        return [int4_matmul(*c) for c in cases] + int4_matmul_grouped(xg, [(pg, sg), (pg2, sg2)])
+
     with torch.cuda.stream(s):
-        for c in cases:   # warm up on the capture stream: creates its workspace
-            int4_matmul(*c)
+        body()  # warm up on the capture stream: creates its workspace
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=s):
-        outs = [int4_matmul(*c) for c in cases]
+        outs = body()
     for rep in range(4):
         for o in outs:
             o.zero_()
