@@ -1,25 +1,36 @@
 #!/usr/bin/env python3
 """W4A16 benchmark on one MI355X: HBM GB/s at M=1 and MFMA TFLOP/s at M=2048.
 
-Step = one Qwen3-8B decode sweep at M=1: 36 layers x 7 projections (q, k, v, o,
-gate, up, down), each a separate ``int4_matmul`` call on that layer's own
-weights (3.69 GB of INT4 weights + scales, so nothing is served from the
-256 MB Infinity Cache), captured once as a HIP graph and replayed.  ``value`` is
-the sweep's algorithmic bytes / wall time per step, with everything resident in
-HBM before the timed region.
+Step = one Qwen3-8B decode sweep at M=1 (config 2): 36 layers x 7 projections
+(q, k, v, o, gate, up, down), each a separate ``int4_matmul`` call on that
+layer's own weights, which is the reference's own call pattern
+(engine/llama_attention.py:83-85, engine/llama_mlp.py:30-33).  The 3.69 GB of
+INT4 weights + scales exceed the 256 MB Infinity Cache, so every step streams
+them from HBM.  The sweep is captured once as a HIP graph and replayed; inputs
+are resident in HBM before the timed region.  ``value`` = algorithmic bytes of
+the sweep / time per step.
 
-Printed as one JSON line, with:
-  roofline      the skinny kernel on gate_proj (K=4096, N=12288, M=1): algorithmic
-                bytes per launch / average launch duration (HIP events around a
-                graph of 36 back-to-back launches on distinct layers), against
-                8 TB/s HBM.
-  prefill       one Qwen3-8B layer at M=2048 (7 projections, config 4): TFLOP/s
-                against 2.5 PFLOP/s dense bf16, plus the gate_proj GEMM alone.
-  cpu_baseline  the reference's host path (dequantize with bf16 scales, then
-                x @ w in bf16, engine/kernels/quant.py:264-266) restated in
-                oracle/int4_oracle.cpu_path, timed on this host for one layer.
+The JSON line also carries:
+  fused_sweep     the same 36 layers through ``int4_matmul_grouped``: q/k/v in
+                  one launch, o, gate+up in one launch, down (4 launches/layer).
+  per_projection  M=1 launch durations per projection.
+  batched_decode  config 3: M in {4, 8, 16, 32} at gate/up and down.
+  prefill         config 4: the seven projections at M=2048, per projection and
+                  as a layer (drop-in and grouped), TFLOP/s vs 2.5 PFLOP/s.
+  roofline        decode kernel on gate_proj (K=4096, N=12288, M=1): algorithmic
+                  bytes per launch / average launch duration, against 8 TB/s.
+  roofline_prefill  the GEMM on gate_proj at M=2048 against dense bf16 MFMA peak.
+  cpu_baseline    the reference's host path (dequantize with bf16 scales, then
+                  x @ w in bf16, engine/kernels/quant.py:264-266), restated in
+                  oracle/int4_oracle.cpu_path, timed on this host.
+
+Launch durations are HIP events on the launch stream around a graph of 36
+back-to-back launches on distinct weights, divided by 36, so they include the
+~1-2 us dispatch gap between graph kernels; rocprofv3's per-kernel average
+excludes that gap.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
+    python bench.py --kernels-only [--copy-calibration]   # roofline kernels only (for rocprofv3)
 """
 
 from __future__ import annotations
@@ -27,6 +38,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -39,6 +51,9 @@ for _p in (ROOT, os.path.join(ROOT, "inf-engine_amd")):
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = "W4A16 GEMM: HBM GB/s (% of peak) at M=1; MFMA TFLOPS (% peak) at M=2048"
+LAUNCHES = 36  # distinct weight sets per timed graph (one per layer)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemv_gate_m1.md")
+TRAFFIC_FILE_PREFILL = os.path.join(ROOT, "profiles", "traffic_gemm_gate_m2048.md")
 
 
 def log(msg: str) -> None:
@@ -76,35 +91,153 @@ def time_graph(g, stream, reps: int) -> float:
     return start.elapsed_time(end) / reps
 
 
-def cpu_baseline(host_layer, k_model: int) -> dict:
+def time_launches(fn, stream, reps: int = 10) -> float:
+    """us per launch of `fn` (which issues LAUNCHES launches), from a captured graph."""
+    g, _ = capture(fn, stream)
+    for _ in range(3):
+        g.replay()
+    us = time_graph(g, stream, reps) * 1e3 / LAUNCHES
+    del g
+    return us
+
+
+def read_traffic(path: str):
+    """HBM bytes per launch recorded by the rocprofv3 --pmc summary at `path` (or None)."""
+    try:
+        with open(path) as f:
+            text = f.read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", text, re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(host_layer, budget_s: float) -> dict:
+    """The reference's host path over the 7 projections of one layer at M=1,
+    repeated until `budget_s` seconds of CPU work have run."""
     import torch
 
     from oracle import int4_oracle as orc
     from w4a16 import synth
 
     threads = torch.get_num_threads()
-    total_s = 0.0
-    total_bytes = 0
-    for name, k, n, packed, scale in host_layer:
-        x = synth.make_activations(1, k, seed=5)
-        orc.cpu_path(x, packed, scale)  # warmup
-        times = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            orc.cpu_path(x, packed, scale)
-            times.append(time.perf_counter() - t0)
-        total_s += statistics.median(times)
-        total_bytes += synth.algorithmic_bytes(1, k, n)
+    xs = {k: synth.make_activations(1, k, seed=5) for _, k, _, _, _ in host_layer}
+    for _, k, _, packed, scale in host_layer:  # warmup
+        orc.cpu_path(xs[k], packed, scale)
+    layer_bytes = sum(synth.algorithmic_bytes(1, k, n) for _, k, n, _, _ in host_layer)
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        for _, k, _, packed, scale in host_layer:
+            orc.cpu_path(xs[k], packed, scale)
+        passes += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= budget_s:
+            break
     return {
-        "value": round(total_bytes / total_s / 1e9, 3),
+        "value": round(passes * layer_bytes / elapsed / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
         "sample": (
-            "one Qwen3-8B layer at M=1 (7 projections, 102.6 MB), median of 3 runs after 1 warmup per "
-            f"projection, {total_s * 1e3:.1f} ms per layer; the 36-layer sweep is 36x this"
+            f"{passes} passes over one Qwen3-8B layer at M=1 (7 projections, {layer_bytes / 1e6:.1f} MB of int4 "
+            f"weights + scales + x + y each) in {elapsed:.1f} s on {threads} torch threads; the 36-layer sweep "
+            "would take 36x as long per step"
         ),
     }
+
+
+def make_layers(layers: int, shapes, dev):
+    from w4a16 import synth
+
+    return [
+        [synth.make_weight(k, n, seed=1000 * layer + i, device=dev) for i, (_, k, n) in enumerate(shapes)]
+        for layer in range(layers)
+    ]
+
+
+def decode_gate_us(weights, xs, stream) -> float:
+    from w4a16 import int4_matmul
+
+    gi = 4  # gate_proj
+    return time_launches(lambda: [int4_matmul(xs[4096], *weights[l][gi]) for l in range(LAUNCHES)], stream)
+
+
+def prefill_gate_us(weights, xp, stream) -> float:
+    from w4a16 import int4_matmul
+
+    gi = 4
+    return time_launches(lambda: [int4_matmul(xp[4096], *weights[l][gi]) for l in range(LAUNCHES)], stream, reps=3)
+
+
+def roofline_decode(us: float) -> dict:
+    from w4a16 import synth
+
+    b = synth.algorithmic_bytes(1, 4096, 12288)
+    ach = b / (us * 1e-6) / 1e9
+    return {
+        "bound": "hbm",
+        "achieved": round(ach, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(ach / HBM_PEAK_GBS, 4),
+        "traffic": read_traffic(TRAFFIC_FILE),
+        "kernel": "gemv_kernel<8, true> (gate_proj K=4096 N=12288 M=1, one launch of int4_matmul)",
+        "bytes_per_launch": b,
+        "avg_launch_us": round(us, 3),
+    }
+
+
+def roofline_prefill(us: float) -> dict:
+    from w4a16 import synth
+
+    f = synth.algorithmic_flops(2048, 4096, 12288)
+    ach = f / (us * 1e-6) / 1e12
+    return {
+        "bound": "mfma",
+        "achieved": round(ach, 1),
+        "peak": BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(ach / BF16_PEAK_TFLOPS, 4),
+        "traffic": read_traffic(TRAFFIC_FILE_PREFILL),
+        "kernel": "gemm_kernel<4, true> (gate_proj K=4096 N=12288 M=2048), after rowsum_kernel",
+        "flops_per_launch": f,
+        "avg_launch_us": round(us, 3),
+    }
+
+
+def kernels_only(args) -> int:
+    """Only the roofline kernels (and optionally a copy of known size), for rocprofv3."""
+    import torch
+
+    from w4a16 import _native, synth
+
+    _native.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream()
+    if args.copy_calibration:
+        # 256 MiB device-to-device copy: FETCH_SIZE / WRITE_SIZE of this dispatch
+        # calibrate the counters against a known byte count.
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 3 x {src.numel() * 4} bytes read and written")
+        del src, dst
+    gi = 4
+    weights = [[None] * 4 + [synth.make_weight(4096, 12288, seed=1000 * l + gi, device=dev)] for l in range(LAUNCHES)]
+    xs = {4096: synth.make_activations(1, 4096, seed=4096, device=dev)}
+    us = decode_gate_us(weights, xs, stream)
+    log(f"decode gate M=1: {us:.2f} us/launch")
+    out = {"decode_gate_m1": roofline_decode(us)}
+    if not args.no_prefill:
+        xp = {4096: synth.make_activations(2048, 4096, seed=4097, device=dev)}
+        us_p = prefill_gate_us(weights, xp, stream)
+        log(f"prefill gate M=2048: {us_p:.2f} us/launch")
+        out["prefill_gate_m2048"] = roofline_prefill(us_p)
+    print(json.dumps(out), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -113,8 +246,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--kernels-only", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
@@ -123,27 +259,30 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+    if args.kernels_only:
+        return kernels_only(args)
 
     import torch
 
-    from w4a16 import _native, int4_matmul, synth
+    from w4a16 import _native, int4_matmul, int4_matmul_grouped, synth
 
     _native.load_library()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     layers = args.layers
     shapes = synth.QWEN3_8B
+    names = [s[0] for s in shapes]
+    ix = {name: i for i, name in enumerate(names)}
 
     # ---- weights: one distinct INT4 set per layer, resident in HBM ----
     t0 = time.perf_counter()
-    weights = []
-    for layer in range(layers):
-        weights.append([synth.make_weight(k, n, seed=1000 * layer + i, device=dev) for i, (_, k, n) in enumerate(shapes)])
+    weights = make_layers(layers, shapes, dev)
     xs = {k: synth.make_activations(1, k, seed=k, device=dev) for k in {k for _, k, _ in shapes}}
     torch.cuda.synchronize()
     log(f"generated {layers} layers of weights in {time.perf_counter() - t0:.1f}s")
 
     step_bytes = layers * sum(synth.algorithmic_bytes(1, k, n) for _, k, n in shapes)
+    stream = torch.cuda.Stream()
 
     def sweep():
         outs = []
@@ -152,9 +291,18 @@ def main() -> int:
                 outs.append(int4_matmul(xs[k], packed, scale))
         return outs
 
-    stream = torch.cuda.Stream()
-    g_sweep, _ = capture(sweep, stream)
+    def fused_layer(w, x4096, x12288):
+        qkv = int4_matmul_grouped(x4096, [w[ix["q_proj"]], w[ix["k_proj"]], w[ix["v_proj"]]])
+        o = int4_matmul(x4096, *w[ix["o_proj"]])
+        gu = int4_matmul_grouped(x4096, [w[ix["gate_proj"]], w[ix["up_proj"]]])
+        d = int4_matmul(x12288, *w[ix["down_proj"]])
+        return qkv + [o] + gu + [d]
 
+    def fused_sweep():
+        return [fused_layer(weights[l], xs[4096], xs[12288]) for l in range(layers)]
+
+    # ---- headline: drop-in sweep ----
+    g_sweep, _ = capture(sweep, stream)
     for _ in range(args.warmup):
         g_sweep.replay()
     torch.cuda.synchronize()
@@ -170,79 +318,91 @@ def main() -> int:
     wall = time.perf_counter() - wall0
     ms_per_step = start.elapsed_time(end) / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    del g_sweep
     log(f"sweep: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s (wall {wall * 1e3 / args.steps:.1f} ms/step)")
 
-    # ---- per-projection launch durations (graph of `layers` launches each) ----
+    g_fused, _ = capture(fused_sweep, stream)
+    for _ in range(args.warmup):
+        g_fused.replay()
+    fms = time_graph(g_fused, stream, args.steps)
+    del g_fused
+    fused = {
+        "ms_per_step": round(fms, 5),
+        "GB/s": round(step_bytes / (fms * 1e-3) / 1e9, 1),
+        "frac_of_hbm_peak": round(step_bytes / (fms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "launches_per_step": 4 * layers,
+    }
+    log(f"fused sweep: {fms * 1e3:.1f} us/step, {fused['GB/s']} GB/s")
+
+    # ---- per-projection launch durations at M=1 ----
     per_proj = {}
     for i, (name, k, n) in enumerate(shapes):
-        def proj(i=i, k=k):
-            return [int4_matmul(xs[k], *weights[layer][i]) for layer in range(layers)]
-
-        g, _ = capture(proj, stream)
-        for _ in range(3):
-            g.replay()
-        us = time_graph(g, stream, 10) * 1e3 / layers
+        us = time_launches(lambda i=i, k=k: [int4_matmul(xs[k], *weights[l % layers][i]) for l in range(LAUNCHES)],
+                           stream)
         gbs = synth.algorithmic_bytes(1, k, n) / (us * 1e-6) / 1e9
         per_proj[name] = {"us": round(us, 3), "GB/s": round(gbs, 1)}
         log(f"  {name:10s} K={k:5d} N={n:5d}: {us:7.2f} us/launch  {gbs:7.1f} GB/s")
-        del g
-    gate = per_proj["gate_proj"]
-    gate_bytes = synth.algorithmic_bytes(1, 4096, 12288)
-    roofline = {
-        "bound": "hbm",
-        "achieved": gate["GB/s"],
-        "peak": HBM_PEAK_GBS,
-        "unit": "GB/s",
-        "frac": round(gate["GB/s"] / HBM_PEAK_GBS, 4),
-        "traffic": None,
-        "kernel": "skinny_kernel<1,16> (gate_proj K=4096 N=12288 M=1)",
-        "bytes_per_launch": gate_bytes,
-        "avg_launch_us": gate["us"],
-    }
+    roofline = roofline_decode(per_proj["gate_proj"]["us"])
 
-    # ---- prefill: one layer at M=2048 ----
+    # ---- config 3: batched decode / verify ----
+    batched = {}
+    for m in (4, 8, 16, 32):
+        xm = {k: synth.make_activations(m, k, seed=k + m, device=dev) for k in (4096, 12288)}
+        for name in ("gate_proj", "down_proj"):
+            i = ix[name]
+            _, k, n = shapes[i]
+            us = time_launches(lambda i=i, k=k: [int4_matmul(xm[k], *weights[l % layers][i]) for l in range(LAUNCHES)],
+                               stream)
+            gbs = synth.algorithmic_bytes(m, k, n) / (us * 1e-6) / 1e9
+            tf = synth.algorithmic_flops(m, k, n) / (us * 1e-6) / 1e12
+            batched[f"M{m}_{name}"] = {"us": round(us, 3), "GB/s": round(gbs, 1), "TFLOP/s": round(tf, 2)}
+            log(f"  M={m:2d} {name:10s}: {us:7.2f} us/launch  {gbs:7.1f} GB/s  {tf:6.2f} TFLOP/s")
+        del xm
+
+    # ---- config 4: prefill at M=2048 ----
     prefill = None
+    roof_pf = None
     if not args.no_prefill:
         m = 2048
         xp = {k: synth.make_activations(m, k, seed=k + 1, device=dev) for k in {k for _, k, _ in shapes}}
+        proj = {}
+        for i, (name, k, n) in enumerate(shapes):
+            us = time_launches(lambda i=i, k=k: [int4_matmul(xp[k], *weights[l % layers][i]) for l in range(LAUNCHES)],
+                               stream, reps=3)
+            tf = synth.algorithmic_flops(m, k, n) / (us * 1e-6) / 1e12
+            proj[name] = {"us": round(us, 2), "TFLOP/s": round(tf, 1)}
+            log(f"  prefill {name:10s}: {us:8.2f} us  {tf:7.1f} TFLOP/s")
+        flops = sum(synth.algorithmic_flops(m, k, n) for _, k, n in shapes)
 
         def layer_fn():
-            return [int4_matmul(xp[k], *weights[0][i]) for i, (_, k, n) in enumerate(shapes)]
+            return [int4_matmul(xp[k], *weights[l][i]) for l in range(4) for i, (_, k, n) in enumerate(shapes)]
 
-        g, _ = capture(layer_fn, stream)
-        for _ in range(3):
+        def layer_fused():
+            return [fused_layer(weights[l], xp[4096], xp[12288]) for l in range(4)]
+
+        res = {}
+        for tag, fn in (("drop_in", layer_fn), ("grouped", layer_fused)):
+            g, _ = capture(fn, stream)
             g.replay()
-        ms = time_graph(g, stream, max(3, args.steps // 2))
-        flops = sum(synth.algorithmic_flops(m, k, n) for _, k, n in shapes)
-        tflops = flops / (ms * 1e-3) / 1e12
-        del g
-        gi = 4  # gate_proj
-
-        def gate_fn():
-            return [int4_matmul(xp[4096], *weights[layer][gi]) for layer in range(4)]
-
-        g, _ = capture(gate_fn, stream)
-        g.replay()
-        gms = time_graph(g, stream, 5) / 4
-        gtf = synth.algorithmic_flops(m, 4096, 12288) / (gms * 1e-3) / 1e12
-        del g
+            ms = time_graph(g, stream, 3) / 4
+            del g
+            res[tag] = {"us_per_layer": round(ms * 1e3, 1), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
+            log(f"prefill layer ({tag}): {ms * 1e3:.1f} us, {res[tag]['TFLOP/s']} TFLOP/s")
         prefill = {
-            "workload": "qwen3-8b layer, M=2048, 7 projections",
-            "ms_per_layer": round(ms, 4),
-            "tflops": round(tflops, 2),
-            "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
-            "gate_proj_us": round(gms * 1e3, 2),
-            "gate_proj_tflops": round(gtf, 2),
+            "workload": "qwen3-8b, M=2048, 7 projections",
+            "per_projection": proj,
+            "layer": res,
+            "frac_of_bf16_peak": round(res["drop_in"]["TFLOP/s"] / BF16_PEAK_TFLOPS, 4),
             "peak_tflops": BF16_PEAK_TFLOPS,
         }
-        log(f"prefill layer M=2048: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s; gate {gms * 1e3:.1f} us {gtf:.1f} TFLOP/s")
+        roof_pf = roofline_prefill(proj["gate_proj"]["us"])
         del xp
 
     # ---- CPU baseline: the reference's host path on one layer ----
     cpu = None
     if not args.no_cpu_baseline:
         host_layer = [(name, k, n, p.cpu(), s.cpu()) for (name, k, n), (p, s) in zip(shapes, weights[0])]
-        cpu = cpu_baseline(host_layer, 4096)
+        cpu = cpu_baseline(host_layer, args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
 
     out = {
@@ -259,15 +419,19 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic: seeded N(0,0.02) bf16 weights quantized to int4 (group 128, fp32 scales), N(0,1) bf16 x",
         "config": {
-            "workload": f"qwen3-8b decode M=1, {layers}-layer x 7-projection weight-streaming sweep (one HIP graph)",
+            "workload": f"qwen3-8b decode M=1 (config 2): {layers}-layer x 7-projection weight-streaming sweep, "
+                        "one int4_matmul call per projection, replayed as one HIP graph",
             "M": 1,
             "layers": layers,
             "bytes_per_step": step_bytes,
             "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         },
+        "fused_sweep": fused,
         "per_projection_M1": per_proj,
-        "roofline": roofline,
+        "batched_decode": batched,
         "prefill": prefill,
+        "roofline": roofline,
+        "roofline_prefill": roof_pf,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
