@@ -27,6 +27,7 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kGroup = 128;                      // K rows per scale group
 constexpr int kPackedRowsPerGroup = kGroup / 2;  // packed rows per group
+constexpr uint32_t kBf16ExpBytes = 0x43434343u;  // high byte of bf16(128 + u) in every byte
 constexpr uint32_t kBf16Base = 0x43004300u;      // bf16 128.0 in both halves
 constexpr uint32_t kBf16Neg136 = 0xC308C308u;    // bf16 -136.0 in both halves
 constexpr float kOffset = 136.0f;                // 128 (bf16 base) + 8 (nibble bias)
@@ -54,26 +55,31 @@ __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// A 32-bit word of packed bytes (4 columns) prepared for pair extraction.
+// A 32-bit word of packed bytes (4 columns) spread to one nibble per byte:
+// byte 2j of x01 / x23 is u = q + 8 of the even row of column j / j+2 (the high
+// nibble), byte 2j+1 that of the odd row (the low nibble).  Every byte holds a
+// clean value 0..15, so one byte permute against 0x43 bytes yields a bf16 pair.
 struct Prep {
-  uint32_t p;  // nibble sign bits flipped: every nibble now holds u = q + 8
-  uint32_t q;  // p >> 4: the high nibble of byte c sits in the low nibble of byte c
+  uint32_t x01;  // columns 0 and 1
+  uint32_t x23;  // columns 2 and 3
 };
 
 __device__ __forceinline__ Prep prep(uint32_t raw) {
+  const uint32_t p = raw ^ 0x88888888u;       // q + 8 in every nibble
+  const uint32_t lo = p & 0x0F0F0F0Fu;        // odd rows
+  const uint32_t hi = (p >> 4) & 0x0F0F0F0Fu;  // even rows
+  // v_perm_b32 byte pool: bytes 0-3 come from the second operand, 4-7 from the first.
   Prep w;
-  w.p = raw ^ 0x88888888u;
-  w.q = w.p >> 4;
+  w.x01 = __builtin_amdgcn_perm(hi, lo, 0x01050004u);
+  w.x23 = __builtin_amdgcn_perm(hi, lo, 0x03070206u);
   return w;
 }
 
-// bf16 pair for byte c (0..3) of a prepared word: low half 128 + u(even row),
-// high half 128 + u(odd row).
+// bf16 pair for byte c (0..3) of the raw word: low half 128 + u(even row),
+// high half 128 + u(odd row); bytes 1 and 3 are the 0x43 exponent byte.
 template <int C>
 __device__ __forceinline__ uint32_t pair_of(Prep w) {
-  // v_perm_b32 byte pool: bytes 0-3 come from the second operand, 4-7 from the first.
-  const uint32_t y = __builtin_amdgcn_perm(w.p, w.q, (uint32_t)C | ((uint32_t)(4 + C) << 16));
-  return (y & 0x000F000Fu) | kBf16Base;
+  return __builtin_amdgcn_perm(C < 2 ? w.x01 : w.x23, kBf16ExpBytes, (C & 1) ? 0x00070006u : 0x00050004u);
 }
 
 __device__ __forceinline__ uint32_t pair_dyn(Prep w, int c) {
