@@ -165,19 +165,13 @@ struct DecodeSlot {
   float s[CPL];
 };
 
-// xs: LDS activations [M][kpitch] bf16; g_local = group index within the staged K range.
+// One group of one wave: A[st] are the activation fragments of the group's 4
+// K steps (rows past M zero), d the group's packed weights and scales.
 template <int CPL>
-__device__ __forceinline__ void decode_compute(const DecodeSlot<CPL>& d, const uint16_t* xs, int kpitch, int g_local,
-                                               int xrow_idx, int lk, f32x4_t (&total)[CPL]) {
+__device__ __forceinline__ void decode_group(const DecodeSlot<CPL>& d, const bf16x8_t (&A)[4],
+                                             f32x4_t (&total)[CPL]) {
   constexpr int WPR = CPL / 4;
   const bf16x8_t neg136 = as_bf16x8(u32x4_t{kBf16Neg136, kBf16Neg136, kBf16Neg136, kBf16Neg136});
-  const uint16_t* xrow = xs + xrow_idx * kpitch + g_local * kGroup + lk * 8;
-  bf16x8_t A[4];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xrow + st * 32);
-    A[st] = as_bf16x8(v);
-  }
   f32x4_t cinit = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int st = 0; st < 4; ++st) cinit = mfma16(A[st], neg136, cinit);
@@ -204,9 +198,19 @@ __device__ __forceinline__ void decode_compute(const DecodeSlot<CPL>& d, const u
     for (int r = 0; r < 4; ++r) total[t][r] = __builtin_fmaf(acc[t][r], d.s[t], total[t][r]);
 }
 
-template <int CPL, bool FULL, int DEPTH>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DEPTH == 1 ? 3 : 2, 8))) void gemv_kernel(
-    Launch L) {
+// xs: LDS activations [M][kpitch] bf16; g_local = group index within the staged K range.
+template <int CPL>
+__device__ __forceinline__ void decode_compute(const DecodeSlot<CPL>& d, const uint16_t* xs, int kpitch, int g_local,
+                                               int xrow_idx, int lk, f32x4_t (&total)[CPL]) {
+  const uint16_t* xrow = xs + xrow_idx * kpitch + g_local * kGroup + lk * 8;
+  bf16x8_t A[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) A[st] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(xrow + st * 32));
+  decode_group<CPL>(d, A, total);
+}
+
+template <int CPL, bool FULL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void gemv_kernel(Launch L) {
   constexpr int WCOLS = 16 * CPL;
   extern __shared__ __attribute__((aligned(16))) float smem[];
 
@@ -234,13 +238,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DEPTH == 1 
   // whose per-lane offset (column, k-block row) is fixed and whose row is a
   // scalar offset, so no per-load address arithmetic is needed.
   int g = g_begin + wave;
-  DecodeSlot<CPL> slot[DEPTH];
+  DecodeSlot<CPL> slot;
   const uint32_t ldp = (uint32_t)P.ldp;
   const __amdgpu_buffer_rsrc_t wrs = make_rsrc(P.packed, (uint32_t)((size_t)(P.K / 2) * P.ldp));
   const __amdgpu_buffer_rsrc_t srs = make_rsrc(P.scale, (uint32_t)((size_t)G * P.lds * 4));
   const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
   const uint32_t svoff = (uint32_t)col0 * 4u;
-  auto load_group = [&](DecodeSlot<CPL>& cur, int gg) {
+  auto load_group = [&](int gg) {
+    DecodeSlot<CPL>& cur = slot;
     if constexpr (FULL) {
       const uint32_t gbase = (uint32_t)gg * kPackedRowsPerGroup * ldp;
 #pragma unroll
@@ -266,8 +271,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DEPTH == 1 
       load_scales<CPL, false>(P.scale + (int64_t)gg * P.lds, col0, N, (P.vec & 1) != 0, cur.s);
     }
   };
-  if (g < g_end) load_group(slot[0], g);
-  if (DEPTH == 2 && g + 4 < g_end) load_group(slot[DEPTH - 1], g + 4);
+  if (g < g_end) load_group(g);
   W4A16_MARK(1);
 
   // Activations of the workgroup's K range -> LDS.
@@ -292,32 +296,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DEPTH == 1 
   f32x4_t total[CPL];
 #pragma unroll
   for (int t = 0; t < CPL; ++t) total[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  if constexpr (DEPTH == 1) {
-    while (g < g_end) {
-#ifdef W4A16_ABL_NOCOMPUTE
-      {
-        uint32_t h = 0;
-        for (int a = 0; a < 4; ++a) for (int b = 0; b < 4; ++b) for (int c = 0; c < CPL / 4; ++c) h ^= slot[0].raw[a][b][c];
-        total[0][0] += (float)h;
-      }
-#else
-      decode_compute<CPL>(slot[0], xs, kpitch, g - g_begin, xrow_idx, lk, total);
-#endif
-      g += 4;
-      if (g < g_end) load_group(slot[0], g);
-    }
-  } else {
-    // Two groups in flight per wave: the loads of group g + 8 are issued as
-    // soon as group g has been consumed.
-    while (g < g_end) {
-      decode_compute<CPL>(slot[0], xs, kpitch, g - g_begin, xrow_idx, lk, total);
-      if (g + 8 < g_end) load_group(slot[0], g + 8);
-      g += 4;
-      if (g >= g_end) break;
-      decode_compute<CPL>(slot[1], xs, kpitch, g - g_begin, xrow_idx, lk, total);
-      if (g + 8 < g_end) load_group(slot[1], g + 8);
-      g += 4;
-    }
+  while (g < g_end) {
+    decode_compute<CPL>(slot, xs, kpitch, g - g_begin, xrow_idx, lk, total);
+    g += 4;
+    if (g < g_end) load_group(g);
   }
   W4A16_MARK(3);
 
@@ -348,10 +330,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DEPTH == 1 
     W4A16_MARK(5);
     return;
   }
-#ifdef W4A16_ABL_NOFINISH
-  if (threadIdx.x < elems && wave_sum(threadIdx.x) == 1.2345f) P.y[0] = 1;
-  return;
-#endif
   splitk_finish<256>(P, M, split, strip, n0, WCOLS, M, wave_sum);
   W4A16_MARK(6);
 }
@@ -905,7 +883,6 @@ int env_int(const char* name, int dflt) {
 struct Plan {
   Kind kind;
   int cpl;
-  int depth;           // gemv: groups in flight per wave
   bool full;           // every problem takes the unconditional (aligned, full tile) load path
   size_t lds_bytes;    // dynamic LDS (gemv / skinny)
   size_t ws_bytes;
@@ -970,7 +947,6 @@ Plan make_plan(const w4a16_problem* probs, int count, int M) {
         if (probs[i].N % 128 != 0) cpl = 4;
     }
     pl.cpl = cpl;
-    pl.depth = env_int("W4A16_DEPTH", 1);
     const int wcols = 16 * cpl;
     int wg = 0;
     size_t lds = 0;
@@ -1088,12 +1064,12 @@ int launch_status() {
   return e == hipSuccess ? W4A16_OK : W4A16_ERR_LAUNCH;
 }
 
-template <int CPL, int DEPTH>
+template <int CPL>
 int launch_gemv(const Plan& pl, hipStream_t s) {
   if (pl.full)
-    hipLaunchKernelGGL((gemv_kernel<CPL, true, DEPTH>), dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
+    hipLaunchKernelGGL((gemv_kernel<CPL, true>), dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
   else
-    hipLaunchKernelGGL((gemv_kernel<CPL, false, DEPTH>), dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
+    hipLaunchKernelGGL((gemv_kernel<CPL, false>), dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
   return launch_status();
 }
 
@@ -1150,10 +1126,7 @@ int run(const w4a16_problem* probs, int count, int M, void* workspace, size_t wo
   if (pl.too_many_counters) return W4A16_ERR_TOO_LARGE;
   if (pl.ws_bytes > 0 && (!workspace || workspace_bytes < pl.ws_bytes)) return W4A16_ERR_WORKSPACE;
   bind(pl, workspace);
-  if (pl.kind == kGemv) {
-    if (pl.depth == 2) return pl.cpl == 4 ? launch_gemv<4, 2>(pl, s) : launch_gemv<8, 2>(pl, s);
-    return pl.cpl == 4 ? launch_gemv<4, 1>(pl, s) : launch_gemv<8, 1>(pl, s);
-  }
+  if (pl.kind == kGemv) return pl.cpl == 4 ? launch_gemv<4>(pl, s) : launch_gemv<8>(pl, s);
   if (pl.kind == kSkinny) {
     if (pl.full)
       hipLaunchKernelGGL(skinny_kernel<true>, dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
