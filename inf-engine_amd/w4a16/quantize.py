@@ -123,6 +123,21 @@ class QuantizedLlamaWeights:
         return out
 
 
+def _block_suffixes(config) -> list[str]:
+    """Projection names inside one decoder block (engine/quantize.py:37-48, 172-217)."""
+    names = list(_LINEAR_SUFFIXES)
+    if getattr(config, "is_moe", False):
+        names += [f"mlp.shared_expert.{p}" for p in _EXPERT_PROJ_SUFFIXES]
+        for j in range(config.n_experts):
+            names += [f"mlp.experts.{j}.{p}" for p in _EXPERT_PROJ_SUFFIXES]
+    return names
+
+
+def projection_keys(config) -> list[str]:
+    """Flat weight names of every projection ``quantize_llama`` may quantize."""
+    return [f"model.layers.{i}.{s}" for i in range(config.n_layer) for s in _block_suffixes(config)]
+
+
 def quantize_llama(model, group_size: int = 128):
     """Quantize every linear projection of ``model`` to INT4 W4A16 (engine/quantize.py:155-242).
 
@@ -141,12 +156,7 @@ def quantize_llama(model, group_size: int = 128):
     for i in range(config.n_layer):
         prefix = f"model.layers.{i}."
         block = orig.layer(i)
-        names = list(_LINEAR_SUFFIXES)
-        if getattr(config, "is_moe", False):
-            names += [f"mlp.shared_expert.{p}" for p in _EXPERT_PROJ_SUFFIXES]
-            for j in range(config.n_experts):
-                names += [f"mlp.experts.{j}.{p}" for p in _EXPERT_PROJ_SUFFIXES]
-        for suffix in names:
+        for suffix in _block_suffixes(config):
             w = block.get(suffix)
             if w is None:
                 continue

@@ -313,6 +313,25 @@ def test_quantize_llama_on_device_matches_dense():
                     "down_proj M=40")
 
 
+def test_int4_checkpoint_loads_to_device_and_matches(tmp_path):
+    """save_int4 -> load_quantized_llama(device=cuda): identical bytes, identical outputs."""
+    from w4a16 import linear, load_quantized_llama, quantize_llama, quantized_to_device, save_int4
+    from test_host import _mini_model
+
+    say("int4 checkpoint round trip on device")
+    model, _ = _mini_model(d=512, f=768, layers=1, kv=256)
+    q = quantized_to_device(quantize_llama(model, 128), DEV)
+    path = str(tmp_path / "q.safetensors")
+    save_int4(q, path)
+    fresh, _ = _mini_model(d=512, f=768, layers=1, kv=256)
+    q2 = load_quantized_llama(fresh, path, device=DEV)
+    x = torch.randn(3, 512).bfloat16().to(DEV)
+    for suffix in ("self_attn.q_proj.weight", "mlp.up_proj.weight"):
+        a, b = q.w.layer(0)[suffix], q2.w.layer(0)[suffix]
+        assert b.packed.is_cuda and torch.equal(a.packed, b.packed) and torch.equal(a.scale, b.scale)
+        assert torch.equal(linear(x, a), linear(x, b))
+
+
 def test_graph_capture_replays_match_eager():
     """int4_matmul captured in a HIP graph: each replay, separated by eager work
     and synchronisation, must reproduce the eager result bit for bit."""
