@@ -25,10 +25,10 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 2
+#define W4A16_ABI_VERSION 3
 
 /* Most problems one grouped call accepts. */
-#define W4A16_MAX_PROBLEMS 8
+#define W4A16_MAX_PROBLEMS 16
 
 /* Status codes. */
 #define W4A16_OK 0
@@ -46,8 +46,9 @@ extern "C" {
 #define W4A16_DTYPE_BF16 1
 
 /*
- * One projection y[M, N] = x[M, K] @ W[K, N] of a grouped call (all problems
- * of a call share M).  Layouts as for w4a16_linear.
+ * One projection y[M, N] = x[M, K] @ W[K, N] of a grouped call.  Layouts as
+ * for w4a16_linear; every problem has its own M (a set of MoE experts with
+ * their own token counts) or the same (q/k/v, gate/up).
  */
 typedef struct w4a16_problem {
   const void* x;        /* bf16 [M, K] */
@@ -58,6 +59,7 @@ typedef struct w4a16_problem {
   int64_t lds;
   void* y;              /* bf16 [M, N] */
   int64_t ldy;
+  int M;
   int N;
   int K;
 } w4a16_problem;
@@ -102,23 +104,25 @@ int w4a16_linear(const void* x, int64_t ldx,
                  void* stream);
 
 /*
- * Several independent projections in one launch: up to W4A16_MAX_PROBLEMS
- * problems sharing M, each with its own activations, weights and output
- * (problems may share x, e.g. q/k/v or gate/up of a decoder block).  Same
- * arithmetic and status codes as w4a16_linear; the workspace must be at least
- * w4a16_workspace_size_grouped() for the same table.
+ * Several independent projections: up to W4A16_MAX_PROBLEMS problems, each
+ * with its own M, activations, weights and output (problems may share x, e.g.
+ * q/k/v or gate/up of a decoder block).  Problems with M <= 16 run in one
+ * decode launch and problems with M > 32 in one GEMM launch; 16 < M <= 32
+ * problems launch one at a time.  Same arithmetic and status codes as
+ * w4a16_linear; the workspace must be at least w4a16_workspace_size_grouped()
+ * for the same table.
  *
  * No counterpart in the reference, which calls int4_matmul once per projection
- * (engine/llama_attention.py:83-85, engine/llama_mlp.py:30-33,
- * engine/llama_moe.py:90-105).  It is the fused-projection path for those call
- * sites: one launch streams all the listed weights.
+ * (engine/llama_attention.py:83-85, engine/llama_mlp.py:30-33) and once per
+ * active expert and projection (engine/llama_moe.py:90-105).  It is the
+ * fused-projection path for those call sites: one launch streams all the
+ * listed weights.
  */
-int w4a16_linear_grouped(const w4a16_problem* problems, int count, int M, int group_size,
+int w4a16_linear_grouped(const w4a16_problem* problems, int count, int group_size,
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes w4a16_linear_grouped needs for this problem table. */
-int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int M, int group_size,
-                                 size_t* bytes);
+int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int group_size, size_t* bytes);
 
 /*
  * out[K, N] = q[K, N] * scale[k / group_size, n]  in fp32 (out_dtype

@@ -48,7 +48,7 @@ struct Problem {
   float* part;         // split-K partials [nsplit][M][N] (workspace)
   uint32_t* counters;  // one arrival counter per strip / tile (workspace, zero between calls)
   float* rowsum;       // gemm: 136 * row sums [K/128][M] (workspace, maybe shared)
-  int N, K;
+  int M, N, K;
   int wg_begin;        // first workgroup of this problem in the launch grid
   int rs_begin;        // rowsum_kernel: first workgroup (-1: row sums shared with another problem)
   int tiles_m, tiles_n;  // gemm tile grid; gemv/skinny: tiles_n = column strips
@@ -61,7 +61,6 @@ struct Problem {
 struct Launch {
   Problem p[kMaxProblems];
   int count;
-  int M;
   int total_wgs;
 #ifdef W4A16_EXP
   uint64_t* trace;     // per-wave phase timestamps (experiments only)
@@ -226,7 +225,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
   const int lk = lane >> 4;
   const int n0 = strip * WCOLS;
   const int col0 = n0 + lc * CPL;
-  const int M = L.M, N = P.N;
+  const int M = P.M, N = P.N;
   const int G = P.K / kGroup;
   const int g_begin = split * P.gps;
   const int g_end = min(G, g_begin + P.gps);
@@ -423,7 +422,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(Launch L) {
   const int lk = lane >> 4;
   const int n0 = strip * WCOLS;
   const int col0 = n0 + lc * kSkinnyCPL;
-  const int M = L.M, N = P.N;
+  const int M = P.M, N = P.N;
   const int G = P.K / kGroup;
   const int g_begin = split * P.gps;
   const int g_end = min(G, g_begin + P.gps);
@@ -478,7 +477,7 @@ __global__ __launch_bounds__(256) void rowsum_kernel(Launch L) {
   for (int i = 0; i < L.count; ++i)
     if (L.p[i].rs_begin >= 0 && (int)blockIdx.x >= L.p[i].rs_begin) pi = i;
   const Problem& P = L.p[pi];
-  const int M = L.M;
+  const int M = P.M;
   const int G = P.K / kGroup;
   const int64_t item = (int64_t)(blockIdx.x - P.rs_begin) * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
@@ -588,7 +587,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lc = lane & 15;
   const int lk = lane >> 4;
-  const int M = L.M, N = P.N;
+  const int M = P.M, N = P.N;
   const int G = P.K / kGroup;
   const int g_begin = split * P.gps;
   const int g_end = min(G, g_begin + P.gps);
@@ -798,7 +797,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(Launch L) {
   for (int i = 1; i < L.count; ++i)
     if (wg >= L.p[i].red_begin) pi = i;
   const Problem& P = L.p[pi];
-  const int M = L.M, N = P.N;
+  const int M = P.M, N = P.N;
   const int64_t total = (int64_t)M * N;
   const int64_t e0 = (int64_t)(wg - P.red_begin) * kReduceElems + 4 * threadIdx.x;
   if (e0 >= total) return;
@@ -897,10 +896,10 @@ struct Plan {
 };
 
 // Validate one problem; returns a W4A16 status.
-int check_problem(const w4a16_problem& q, int M) {
-  if (q.N < 0 || q.K < 0) return W4A16_ERR_SHAPE;
+int check_problem(const w4a16_problem& q) {
+  if (q.M < 0 || q.N < 0 || q.K < 0) return W4A16_ERR_SHAPE;
   if (q.K % kGroup != 0) return W4A16_ERR_K_GROUP;
-  if (M == 0 || q.N == 0) return W4A16_OK;
+  if (q.M == 0 || q.N == 0) return W4A16_OK;
   if (!q.y) return W4A16_ERR_NULL;
   if (q.K > 0 && (!q.x || !q.packed || !q.scale)) return W4A16_ERR_NULL;
   if (q.ldy < q.N || (q.K > 0 && (q.ldx < q.K || q.ldp < q.N || q.lds < q.N))) return W4A16_ERR_SHAPE;
@@ -909,12 +908,16 @@ int check_problem(const w4a16_problem& q, int M) {
 
 bool gemm_x_ok(const w4a16_problem& q) { return aligned(q.x, 16) && q.ldx % 8 == 0; }
 
-// Plan a launch over problems that all have M > 0, N > 0, K > 0.
-Plan make_plan(const w4a16_problem* probs, int count, int M) {
+inline Kind kind_of(int M) { return M <= 16 ? kGemv : (M <= 32 ? kSkinny : kGemm); }
+
+// Plan one launch over problems that all have M > 0, N > 0, K > 0 and the
+// same kind (kind_of(M)); the skinny kernel takes a single problem.
+Plan make_plan(const w4a16_problem* probs, int count) {
   Plan pl{};
   pl.L.count = count;
-  pl.L.M = M;
-  pl.kind = M <= 16 ? kGemv : (M <= 32 ? kSkinny : kGemm);
+  int max_m = 0;
+  for (int i = 0; i < count; ++i) max_m = std::max(max_m, probs[i].M);
+  pl.kind = kind_of(max_m);
   bool full = true;
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = probs[i];
@@ -927,6 +930,7 @@ Plan make_plan(const w4a16_problem* probs, int count, int M) {
     P.lds = q.lds;
     P.y = static_cast<uint16_t*>(q.y);
     P.ldy = q.ldy;
+    P.M = q.M;
     P.N = q.N;
     P.K = q.K;
     const bool vw = aligned(q.packed, 16) && q.ldp % 16 == 0 && aligned(q.scale, 16) && q.lds % 4 == 0;
@@ -953,6 +957,7 @@ Plan make_plan(const w4a16_problem* probs, int count, int M) {
     for (int i = 0; i < count; ++i) {
       Problem& P = pl.L.p[i];
       const int G = P.K / kGroup;
+      const int M = P.M;
       P.tiles_m = 1;
       P.tiles_n = ceil_div(P.N, wcols);
       if (pl.kind == kGemv) {
@@ -987,15 +992,16 @@ Plan make_plan(const w4a16_problem* probs, int count, int M) {
   } else {
     // GEMM: 256-column tiles unless that leaves the chip under-filled.
     int t4 = 0;
-    for (int i = 0; i < count; ++i) t4 += ceil_div(M, kGemmRows) * ceil_div(probs[i].N, 256);
+    for (int i = 0; i < count; ++i) t4 += ceil_div(probs[i].M, kGemmRows) * ceil_div(probs[i].N, 256);
     pl.cpl = env_int("W4A16_GCPL", t4 < 384 ? 2 : 4);
     const int tcols = 64 * pl.cpl;
     int tiles_total = 0;
-    for (int i = 0; i < count; ++i) tiles_total += ceil_div(M, kGemmRows) * ceil_div(probs[i].N, tcols);
+    for (int i = 0; i < count; ++i) tiles_total += ceil_div(probs[i].M, kGemmRows) * ceil_div(probs[i].N, tcols);
     int wg = 0;
     for (int i = 0; i < count; ++i) {
       Problem& P = pl.L.p[i];
       const int G = P.K / kGroup;
+      const int M = P.M;
       P.tiles_m = ceil_div(M, kGemmRows);
       P.tiles_n = ceil_div(P.N, tcols);
       const int tiles = P.tiles_m * P.tiles_n;
@@ -1016,7 +1022,7 @@ Plan make_plan(const w4a16_problem* probs, int count, int M) {
       // Row sums, shared by problems with the same activations.
       for (int j = 0; j < i; ++j)
         if (probs[j].x == probs[i].x && probs[j].ldx == probs[i].ldx && probs[j].K == probs[i].K &&
-            pl.rowsum_src[j] == j) {
+            probs[j].M == probs[i].M && pl.rowsum_src[j] == j) {
           pl.rowsum_src[i] = j;
           break;
         }
@@ -1083,46 +1089,53 @@ int launch_gemm(const Plan& pl, hipStream_t s) {
   return launch_status();
 }
 
-// Problems that run() launches separately: empty, K == 0, or (M > 32) with
-// activations the GEMM cannot stage with 16-byte copies.
-bool separate(const w4a16_problem& q, int M) { return M == 0 || q.N == 0 || q.K == 0 || (M > 32 && !gemm_x_ok(q)); }
+// Problems that run() launches on their own: K == 0 (zero fill), or M > 32
+// with activations the GEMM cannot stage with 16-byte copies.
+bool separate(const w4a16_problem& q) { return q.K == 0 || (q.M > 32 && !gemm_x_ok(q)); }
 
-int run(const w4a16_problem* probs, int count, int M, void* workspace, size_t workspace_bytes, hipStream_t s) {
-  w4a16_problem live[kMaxProblems];
-  int n = 0;
+// The launches of one call: problems with M > 0 and N > 0 grouped by kernel.
+// Each decode (M <= 16) and GEMM group is one launch; skinny problems
+// (16 < M <= 32) launch one at a time.  Problems in `sep` are handled alone.
+struct Batches {
+  w4a16_problem gemv[kMaxProblems], gemm[kMaxProblems], skinny[kMaxProblems], sep[kMaxProblems];
+  int n_gemv = 0, n_gemm = 0, n_skinny = 0, n_sep = 0;
+};
+
+Batches split(const w4a16_problem* probs, int count) {
+  Batches b;
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = probs[i];
-    if (M == 0 || q.N == 0) continue;
-    if (q.K == 0) {
-      hipLaunchKernelGGL(zero_kernel, dim3(ceil_div((int64_t)M * q.N, 256)), dim3(256), 0, s,
-                         static_cast<uint16_t*>(q.y), q.ldy, M, q.N);
-      const int rc = launch_status();
-      if (rc != W4A16_OK) return rc;
+    if (q.M == 0 || q.N == 0) continue;
+    if (separate(q)) {
+      b.sep[b.n_sep++] = q;
       continue;
     }
-    if (separate(q, M)) {
-      // Unaligned activations with M > 32: 32 rows at a time through the skinny kernel.
-      for (int m0 = 0; m0 < M; m0 += 32) {
-        w4a16_problem c = q;
-        c.x = static_cast<const uint16_t*>(q.x) + (int64_t)m0 * q.ldx;
-        c.y = static_cast<uint16_t*>(q.y) + (int64_t)m0 * q.ldy;
-        const int rc = run(&c, 1, M - m0 < 32 ? M - m0 : 32, workspace, workspace_bytes, s);
-        if (rc != W4A16_OK) return rc;
-      }
-      continue;
+    switch (kind_of(q.M)) {
+      case kGemv: b.gemv[b.n_gemv++] = q; break;
+      case kSkinny: b.skinny[b.n_skinny++] = q; break;
+      default: b.gemm[b.n_gemm++] = q; break;
     }
-    live[n++] = q;
   }
-  if (n == 0) return W4A16_OK;
-  if (M > 16 && M <= 32 && n > 1) {
-    // The skinny kernel takes one problem per launch.
-    for (int i = 0; i < n; ++i) {
-      const int rc = run(&live[i], 1, M, workspace, workspace_bytes, s);
-      if (rc != W4A16_OK) return rc;
-    }
-    return W4A16_OK;
+  return b;
+}
+
+// Unaligned activations with M > 32 go through the skinny kernel 32 rows at a time.
+template <class Fn>
+int for_each_chunk(const w4a16_problem& q, Fn fn) {
+  for (int m0 = 0; m0 < q.M; m0 += 32) {
+    w4a16_problem c = q;
+    c.x = static_cast<const uint16_t*>(q.x) + (int64_t)m0 * q.ldx;
+    c.y = static_cast<uint16_t*>(q.y) + (int64_t)m0 * q.ldy;
+    c.M = q.M - m0 < 32 ? q.M - m0 : 32;
+    const int rc = fn(c);
+    if (rc != W4A16_OK) return rc;
   }
-  Plan pl = make_plan(live, n, M);
+  return W4A16_OK;
+}
+
+// Launch one planned batch (all problems of one kind).
+int launch_plan(const w4a16_problem* probs, int count, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  Plan pl = make_plan(probs, count);
   if (pl.too_many_counters) return W4A16_ERR_TOO_LARGE;
   if (pl.ws_bytes > 0 && (!workspace || workspace_bytes < pl.ws_bytes)) return W4A16_ERR_WORKSPACE;
   bind(pl, workspace);
@@ -1143,46 +1156,64 @@ int run(const w4a16_problem* probs, int count, int M, void* workspace, size_t wo
   return launch_status();
 }
 
-// Workspace run() needs for these problems (0 when none).
-int workspace_for(const w4a16_problem* probs, int count, int M, size_t* bytes) {
-  *bytes = 0;
-  w4a16_problem live[kMaxProblems];
-  int n = 0;
-  for (int i = 0; i < count; ++i) {
-    const w4a16_problem& q = probs[i];
-    if (M == 0 || q.N == 0 || q.K == 0) continue;
-    if (separate(q, M)) {
-      size_t b = 0;
-      const int rc = workspace_for(&q, 1, 32, &b);
-      if (rc != W4A16_OK) return rc;
-      *bytes = std::max(*bytes, b);
-      continue;
-    }
-    live[n++] = q;
-  }
-  if (n == 0) return W4A16_OK;
-  if (M > 16 && M <= 32 && n > 1) {
-    for (int i = 0; i < n; ++i) {
-      size_t b = 0;
-      const int rc = workspace_for(&live[i], 1, M, &b);
-      if (rc != W4A16_OK) return rc;
-      *bytes = std::max(*bytes, b);
-    }
-    return W4A16_OK;
-  }
-  const Plan pl = make_plan(live, n, M);
+// Workspace bytes launch_plan needs for one batch.
+int plan_workspace(const w4a16_problem* probs, int count, size_t* bytes) {
+  const Plan pl = make_plan(probs, count);
   if (pl.too_many_counters) return W4A16_ERR_TOO_LARGE;
   *bytes = std::max(*bytes, pl.ws_bytes);
   return W4A16_OK;
 }
 
-int check_all(const w4a16_problem* probs, int count, int M, int group_size) {
+// The launches run in order on one stream, so they share the workspace.
+int run(const w4a16_problem* probs, int count, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  Batches b = split(probs, count);
+  for (int i = 0; i < b.n_sep; ++i) {
+    const w4a16_problem& q = b.sep[i];
+    int rc;
+    if (q.K == 0) {
+      hipLaunchKernelGGL(zero_kernel, dim3(ceil_div((int64_t)q.M * q.N, 256)), dim3(256), 0, s,
+                         static_cast<uint16_t*>(q.y), q.ldy, q.M, q.N);
+      rc = launch_status();
+    } else {
+      rc = for_each_chunk(q, [&](const w4a16_problem& c) { return launch_plan(&c, 1, workspace, workspace_bytes, s); });
+    }
+    if (rc != W4A16_OK) return rc;
+  }
+  if (b.n_gemv > 0) {
+    const int rc = launch_plan(b.gemv, b.n_gemv, workspace, workspace_bytes, s);
+    if (rc != W4A16_OK) return rc;
+  }
+  for (int i = 0; i < b.n_skinny; ++i) {
+    const int rc = launch_plan(&b.skinny[i], 1, workspace, workspace_bytes, s);
+    if (rc != W4A16_OK) return rc;
+  }
+  if (b.n_gemm > 0) return launch_plan(b.gemm, b.n_gemm, workspace, workspace_bytes, s);
+  return W4A16_OK;
+}
+
+// Workspace run() needs for these problems (0 when none).
+int workspace_for(const w4a16_problem* probs, int count, size_t* bytes) {
+  *bytes = 0;
+  Batches b = split(probs, count);
+  for (int i = 0; i < b.n_sep; ++i) {
+    if (b.sep[i].K == 0) continue;
+    const int rc = for_each_chunk(b.sep[i], [&](const w4a16_problem& c) { return plan_workspace(&c, 1, bytes); });
+    if (rc != W4A16_OK) return rc;
+  }
+  int rc = W4A16_OK;
+  if (b.n_gemv > 0 && (rc = plan_workspace(b.gemv, b.n_gemv, bytes)) != W4A16_OK) return rc;
+  for (int i = 0; i < b.n_skinny; ++i)
+    if ((rc = plan_workspace(&b.skinny[i], 1, bytes)) != W4A16_OK) return rc;
+  if (b.n_gemm > 0 && (rc = plan_workspace(b.gemm, b.n_gemm, bytes)) != W4A16_OK) return rc;
+  return W4A16_OK;
+}
+
+int check_all(const w4a16_problem* probs, int count, int group_size) {
   if (count < 0 || count > kMaxProblems) return W4A16_ERR_SHAPE;
   if (count > 0 && !probs) return W4A16_ERR_NULL;
-  if (M < 0) return W4A16_ERR_SHAPE;
   if (group_size != kGroup) return W4A16_ERR_GROUP_SIZE;
   for (int i = 0; i < count; ++i) {
-    const int rc = check_problem(probs[i], M);
+    const int rc = check_problem(probs[i]);
     if (rc != W4A16_OK) return rc;
   }
   return W4A16_OK;
@@ -1222,31 +1253,31 @@ int w4a16_workspace_size(int M, int N, int K, int group_size, size_t* bytes) {
   // Sized for contiguous, 256-byte aligned operands (what the wrapper passes).
   const uintptr_t a = 256;
   const w4a16_problem q{reinterpret_cast<const void*>(a), K, reinterpret_cast<const int8_t*>(a), N,
-                        reinterpret_cast<const float*>(a), N, reinterpret_cast<void*>(a), N, N, K};
-  return workspace_for(&q, 1, M, bytes);
+                        reinterpret_cast<const float*>(a), N, reinterpret_cast<void*>(a), N, M, N, K};
+  return workspace_for(&q, 1, bytes);
 }
 
-int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int M, int group_size, size_t* bytes) {
+int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int group_size, size_t* bytes) {
   if (!bytes) return W4A16_ERR_NULL;
   *bytes = 0;
-  const int rc = check_all(problems, count, M, group_size);
+  const int rc = check_all(problems, count, group_size);
   if (rc != W4A16_OK) return rc;
-  return workspace_for(problems, count, M, bytes);
+  return workspace_for(problems, count, bytes);
 }
 
-int w4a16_linear_grouped(const w4a16_problem* problems, int count, int M, int group_size, void* workspace,
+int w4a16_linear_grouped(const w4a16_problem* problems, int count, int group_size, void* workspace,
                          size_t workspace_bytes, void* stream) {
-  const int rc = check_all(problems, count, M, group_size);
+  const int rc = check_all(problems, count, group_size);
   if (rc != W4A16_OK) return rc;
-  return run(problems, count, M, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  return run(problems, count, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int w4a16_linear(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, const float* scale, int64_t lds,
                  void* y, int64_t ldy, int M, int N, int K, int group_size, void* workspace, size_t workspace_bytes,
                  void* stream) {
   if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
-  const w4a16_problem q{x, ldx, packed, ldp, scale, lds, y, ldy, N, K};
-  return w4a16_linear_grouped(&q, 1, M, group_size, workspace, workspace_bytes, stream);
+  const w4a16_problem q{x, ldx, packed, ldp, scale, lds, y, ldy, M, N, K};
+  return w4a16_linear_grouped(&q, 1, group_size, workspace, workspace_bytes, stream);
 }
 
 int w4a16_dequant(const int8_t* packed, int64_t ldp, const float* scale, int64_t lds, void* out, int64_t ldo,

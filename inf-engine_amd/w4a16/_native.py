@@ -29,7 +29,7 @@ W4A16_ERR_TOO_LARGE = 8
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
-MAX_PROBLEMS = 8  # W4A16_MAX_PROBLEMS
+MAX_PROBLEMS = 16  # W4A16_MAX_PROBLEMS
 
 # Every symbol include/w4a16.h declares.
 EXPORTED_SYMBOLS = (
@@ -51,7 +51,7 @@ class Problem(ctypes.Structure):
         ("packed", ctypes.c_void_p), ("ldp", ctypes.c_int64),
         ("scale", ctypes.c_void_p), ("lds", ctypes.c_int64),
         ("y", ctypes.c_void_p), ("ldy", ctypes.c_int64),
-        ("N", ctypes.c_int), ("K", ctypes.c_int),
+        ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int),
     ]
 
 _lib = None
@@ -88,9 +88,9 @@ def load_library() -> ctypes.CDLL:
         lib.w4a16_dequant.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
         lib.w4a16_dequant.restype = i32
         pp = ctypes.POINTER(Problem)
-        lib.w4a16_linear_grouped.argtypes = [pp, i32, i32, i32, vp, sz, vp]
+        lib.w4a16_linear_grouped.argtypes = [pp, i32, i32, vp, sz, vp]
         lib.w4a16_linear_grouped.restype = i32
-        lib.w4a16_workspace_size_grouped.argtypes = [pp, i32, i32, i32, ctypes.POINTER(sz)]
+        lib.w4a16_workspace_size_grouped.argtypes = [pp, i32, i32, ctypes.POINTER(sz)]
         lib.w4a16_workspace_size_grouped.restype = i32
         _lib = lib
         return lib
@@ -177,11 +177,10 @@ def linear(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_siz
 
 
 def linear_grouped(xs, weights, group_size: int) -> list[torch.Tensor]:
-    """Several projections in one launch; xs[i] is [M, K_i] bf16, weights[i] = (packed, scale)."""
+    """Several projections in one call; xs[i] is [M_i, K_i] bf16, weights[i] = (packed, scale)."""
     lib = load_library()
     if not 0 < len(weights) <= MAX_PROBLEMS:
         raise ValueError(f"a grouped call takes 1..{MAX_PROBLEMS} projections, got {len(weights)}")
-    m = xs[0].shape[0]
     table = (Problem * len(weights))()
     outs, keep = [], []
     for i, (x, (packed, scale)) in enumerate(zip(xs, weights)):
@@ -192,18 +191,18 @@ def linear_grouped(xs, weights, group_size: int) -> list[torch.Tensor]:
         if scale.stride(1) != 1:
             scale = scale.contiguous()
         keep += [x, packed, scale]
-        n = packed.shape[1]
+        m, n = x.shape[0], packed.shape[1]
         y = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
         outs.append(y)
         table[i] = Problem(x.data_ptr(), x.stride(0), packed.data_ptr(), packed.stride(0), scale.data_ptr(),
-                           scale.stride(0), y.data_ptr(), y.stride(0), n, x.shape[1])
+                           scale.stride(0), y.data_ptr(), y.stride(0), m, n, x.shape[1])
     dev = xs[0].device
     stream = torch.cuda.current_stream(dev).cuda_stream
     nbytes = ctypes.c_size_t(0)
-    check(lib.w4a16_workspace_size_grouped(table, len(weights), m, group_size, ctypes.byref(nbytes)),
+    check(lib.w4a16_workspace_size_grouped(table, len(weights), group_size, ctypes.byref(nbytes)),
           "w4a16_workspace_size_grouped")
     ws = get_workspace(dev, stream, nbytes.value)
-    rc = lib.w4a16_linear_grouped(table, len(weights), m, group_size,
+    rc = lib.w4a16_linear_grouped(table, len(weights), group_size,
                                   ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
                                   stream)
     check(rc, "w4a16_linear_grouped")

@@ -122,21 +122,21 @@ def _check_operands(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, 
 
 
 def int4_matmul_grouped(a, weights, group_size: int = 128) -> list[torch.Tensor]:
-    """Several INT4 projections in one kernel launch: ``[a_i @ dequantize(packed_i, scale_i)]``.
+    """Several INT4 projections at once: ``[a_i @ dequantize(packed_i, scale_i)]``.
 
     ``a`` is one ``(M, K)`` bf16 tensor shared by every projection (q/k/v or
-    gate/up of a block) or a list of per-projection activations with a common
-    M (a set of MoE experts).  ``weights`` is a list of ``(packed, scale)``
-    pairs, at most 8.  Results equal ``int4_matmul`` on each pair up to fp32
-    summation order.  No reference counterpart: the reference calls
-    ``int4_matmul`` once per projection (engine/llama_attention.py:83-85,
-    engine/llama_mlp.py:30-33).
+    gate/up of a block) or a list of per-projection activations, each with its
+    own M (a set of MoE experts with their token counts).  ``weights`` is a list
+    of ``(packed, scale)`` pairs, at most 16.  Projections with M <= 16 share one
+    decode launch and those with M > 32 one GEMM launch.  Results equal
+    ``int4_matmul`` on each pair up to fp32 summation order.  No reference
+    counterpart: the reference calls ``int4_matmul`` once per projection
+    (engine/llama_attention.py:83-85, engine/llama_mlp.py:30-33,
+    engine/llama_moe.py:90-105).
     """
     xs = list(a) if isinstance(a, (list, tuple)) else [a] * len(weights)
     if len(xs) != len(weights):
         raise ValueError("need one activation tensor per weight (or a single shared one)")
-    if len({x.shape[0] for x in xs}) != 1:
-        raise ValueError("all projections of a grouped call must share M")
     prepared = [(packed, _check_operands(x, packed, scale, group_size)) for x, (packed, scale) in zip(xs, weights)]
     with torch.cuda.device(xs[0].device):
         return _native.linear_grouped(xs, prepared, group_size)

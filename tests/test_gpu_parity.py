@@ -266,6 +266,35 @@ def test_grouped_distinct_activations(m):
         check_tolerance(y, orc.fused_reference(x.float().numpy(), p.numpy(), s.numpy()), f"moe K={x.shape[1]}")
 
 
+def test_grouped_mixed_m_across_kernels():
+    """Experts with their own token counts: one table mixes decode (M <= 16),
+    skinny (16 < M <= 32), GEMM (M > 32), an unaligned-x GEMM row block and
+    an empty expert; 16 problems, the table maximum."""
+    from w4a16 import int4_matmul, int4_matmul_grouped, synth
+
+    say("grouped mixed M")
+    ms = [1, 3, 16, 0, 17, 32, 33, 130, 2, 7, 64, 1, 5, 9, 40, 12]
+    k, n = 512, 384
+    weights = [synth.make_weight(k, n, seed=900 + i) for i in range(len(ms))]
+    xs = []
+    for i, m in enumerate(ms):
+        x = synth.make_activations(m, k, seed=950 + i).to(DEV)
+        if i == 14:  # row stride not a multiple of 8 elements: staged through the skinny path
+            buf = torch.zeros(m, k + 3, dtype=torch.bfloat16, device=DEV)
+            buf[:, :k] = x
+            x = buf[:, :k]
+        xs.append(x)
+    dw = [(p.to(DEV), s.to(DEV)) for p, s in weights]
+    outs = int4_matmul_grouped(xs, dw)
+    for i, (m, x, (p, s), y) in enumerate(zip(ms, xs, weights, outs)):
+        assert y.shape == (m, n)
+        if m == 0:
+            continue
+        check_tolerance(y, orc.fused_reference(x.float().cpu().numpy(), p.numpy(), s.numpy()), f"expert {i} M={m}")
+        if m <= 16 and i != 14:  # same decode arithmetic as a lone call
+            assert torch.equal(y, int4_matmul(x, *dw[i]))
+
+
 @pytest.mark.parametrize("m", [1, 20, 64])
 def test_zero_subnormal_and_extreme_scales(m):
     """Zero / subnormal scale groups contribute nothing (exactly on the decode

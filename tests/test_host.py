@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(native_lib):
     assert set(names) == set(_native.EXPORTED_SYMBOLS), names
     for name in names:
         assert hasattr(native_lib, name), name
-    assert native_lib.w4a16_abi_version() == 2
+    assert native_lib.w4a16_abi_version() == 3
 
 
 def _linear(lib, *, x=1, ldx=4096, packed=1, ldp=4096, scale=1, lds=4096, y=1, ldy=4096, m=1, n=4096,
@@ -64,23 +64,34 @@ def test_grouped_argument_validation(native_lib):
     from w4a16 import _native as nat
 
     lib = native_lib
-    table = (nat.Problem * 9)()
-    for i in range(9):
-        table[i] = nat.Problem(1, 4096, 1, 4096, 1, 4096, 1, 4096, 4096, 4096)
+    n_max = nat.MAX_PROBLEMS
+    table = (nat.Problem * (n_max + 1))()
+    for i in range(n_max + 1):
+        table[i] = nat.Problem(1, 4096, 1, 4096, 1, 4096, 1, 4096, 1, 4096, 4096)
     size = ctypes.c_size_t(0)
-    assert lib.w4a16_linear_grouped(table, 9, 1, 128, None, 0, None) == nat.W4A16_ERR_SHAPE
-    assert lib.w4a16_linear_grouped(None, 2, 1, 128, None, 0, None) == nat.W4A16_ERR_NULL
-    assert lib.w4a16_linear_grouped(table, 2, -1, 128, None, 0, None) == nat.W4A16_ERR_SHAPE
-    assert lib.w4a16_linear_grouped(table, 2, 1, 64, None, 0, None) == nat.W4A16_ERR_GROUP_SIZE
-    assert lib.w4a16_linear_grouped(table, 0, 1, 128, None, 0, None) == nat.W4A16_OK
-    bad = (nat.Problem * 2)(table[0], nat.Problem(1, 4096, 1, 4096, 1, 4096, None, 4096, 4096, 4096))
-    assert lib.w4a16_linear_grouped(bad, 2, 1, 128, None, 0, None) == nat.W4A16_ERR_NULL
-    bad[1] = nat.Problem(1, 4096, 1, 4096, 1, 4096, 1, 4096, 4096, 4000)
-    assert lib.w4a16_linear_grouped(bad, 2, 1, 128, None, 0, None) == nat.W4A16_ERR_K_GROUP
+    assert lib.w4a16_linear_grouped(table, n_max + 1, 128, None, 0, None) == nat.W4A16_ERR_SHAPE
+    assert lib.w4a16_linear_grouped(None, 2, 128, None, 0, None) == nat.W4A16_ERR_NULL
+    neg = (nat.Problem * 1)(nat.Problem(1, 4096, 1, 4096, 1, 4096, 1, 4096, -1, 4096, 4096))
+    assert lib.w4a16_linear_grouped(neg, 1, 128, None, 0, None) == nat.W4A16_ERR_SHAPE
+    assert lib.w4a16_linear_grouped(table, 2, 64, None, 0, None) == nat.W4A16_ERR_GROUP_SIZE
+    assert lib.w4a16_linear_grouped(table, 0, 128, None, 0, None) == nat.W4A16_OK
+    bad = (nat.Problem * 2)(table[0], nat.Problem(1, 4096, 1, 4096, 1, 4096, None, 4096, 1, 4096, 4096))
+    assert lib.w4a16_linear_grouped(bad, 2, 128, None, 0, None) == nat.W4A16_ERR_NULL
+    bad[1] = nat.Problem(1, 4096, 1, 4096, 1, 4096, 1, 4096, 1, 4096, 4000)
+    assert lib.w4a16_linear_grouped(bad, 2, 128, None, 0, None) == nat.W4A16_ERR_K_GROUP
+    # A problem with M = 0 is skipped before its pointers are looked at.
+    empty = (nat.Problem * 1)(nat.Problem(None, 4096, None, 4096, None, 4096, None, 4096, 0, 4096, 4096))
+    assert lib.w4a16_linear_grouped(empty, 1, 128, None, 0, None) == nat.W4A16_OK
     # Decode split-K of two problems needs a workspace: sized, then rejected without one.
-    assert lib.w4a16_workspace_size_grouped(table, 2, 1, 128, ctypes.byref(size)) == nat.W4A16_OK
+    assert lib.w4a16_workspace_size_grouped(table, 2, 128, ctypes.byref(size)) == nat.W4A16_OK
     assert size.value >= 65536 + 2 * 8 * 4096 * 4
-    assert lib.w4a16_linear_grouped(table, 2, 1, 128, None, 0, None) == nat.W4A16_ERR_WORKSPACE
+    assert lib.w4a16_linear_grouped(table, 2, 128, None, 0, None) == nat.W4A16_ERR_WORKSPACE
+    # Mixed M: the decode and GEMM batches share one workspace, sized for the larger.
+    mixed = (nat.Problem * 2)(table[0], nat.Problem(16, 4096, 16, 4096, 16, 4096, 16, 4096, 2048, 4096, 4096))
+    assert lib.w4a16_workspace_size_grouped(mixed, 2, 128, ctypes.byref(size)) == nat.W4A16_OK
+    decode_only = ctypes.c_size_t(0)
+    assert lib.w4a16_workspace_size_grouped(table, 1, 128, ctypes.byref(decode_only)) == nat.W4A16_OK
+    assert size.value == max(decode_only.value, nat.workspace_size(2048, 4096, 4096))
 
 
 def test_dequant_argument_validation(native_lib):
