@@ -125,6 +125,20 @@ int w4a16_linear_grouped(const w4a16_problem* problems, int count, int group_siz
 int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int group_size, size_t* bytes);
 
 /*
+ * Dense bf16 GEMV for decode: y[m, n] = sum_k x[m, k] * w[n, k] with w in
+ * Linear layout [N, K] (row stride ldw elements), fp32 accumulation, bf16
+ * output; M <= 16.  x and w must be 16-byte aligned with K, ldx and ldw
+ * multiples of 8.  No workspace.
+ *
+ * Replaces the decode case of `logits = x @ self.w.lm_head.T`
+ * (engine/llama_model.py:148, engine/llama_moe_model.py:206), whose bf16
+ * lm_head the reference leaves unquantized (engine/quantize.py:23).  Returns
+ * W4A16_ERR_TOO_LARGE for M > 16 (callers use a library GEMM there).
+ */
+int w4a16_bf16_gemv(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+                    int M, int N, int K, void* stream);
+
+/*
  * out[K, N] = q[K, N] * scale[k / group_size, n]  in fp32 (out_dtype
  * W4A16_DTYPE_F32), or with scale and product both rounded to bf16
  * (W4A16_DTYPE_BF16), i.e. dequantize_weight_int4(packed, scale.to(dtype))

@@ -823,6 +823,102 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(Launch L) {
 }
 
 // ---------------------------------------------------------------------------
+// Dense bf16 GEMV for the output projection (M <= 16):
+// y[m, n] = sum_k x[m, k] * w[n, k], w in Linear layout [N, K] (row n is the
+// weight vector of output n, contiguous along K), as
+// `logits = x @ lm_head.T` (engine/llama_model.py:148).
+//
+// A wave owns 16 consecutive rows of w and streams them over the whole of K,
+// so no partial leaves the wave.  Per 64-element K chunk a lane issues two
+// 16-byte buffer loads of its row: lane l covers row n0 + l % 16 and bytes
+// 16 * (l / 16) of each 64-byte half, so the 4 lanes of a row read 128
+// contiguous bytes and each 16-byte load is one bf16 B fragment of
+// v_mfma_f32_16x16x32_bf16 as loaded.  kDenseChunks chunks are in flight per
+// lane, double buffered.  x[0:M, :] is staged in LDS with a zero row M for
+// the MFMA rows past M.  Rows past N lie outside the wave's buffer resource
+// and read as zero; they are never stored.
+// ---------------------------------------------------------------------------
+constexpr int kDenseChunks = 4;  // 64-element K chunks per pipeline stage
+
+template <bool FULL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void bf16_gemv_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w, int64_t ldw,
+    uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xsd[];
+  const int kpitch = K + 72;
+  {
+    const int chunks = K / 8;
+    for (int i = threadIdx.x; i < M * chunks; i += 256) {
+      const int m = i / chunks, c = i % chunks;
+      *reinterpret_cast<u32x4_t*>(xsd + m * kpitch + c * 8) =
+          __builtin_bit_cast(u32x4_t, load_x8(x + (int64_t)m * ldx + c * 8, true));
+    }
+    if (M < 16)
+      for (int c = threadIdx.x; c < chunks; c += 256)
+        *reinterpret_cast<u32x4_t*>(xsd + M * kpitch + c * 8) = u32x4_t{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lc = lane & 15;
+  const int lk = lane >> 4;
+  const int n0 = (blockIdx.x * 4 + wave) * 16;
+  if (n0 >= N) return;
+  const int rows = min(16, N - n0);
+  const uint32_t nrec = (uint32_t)((size_t)rows * ldw * 2);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(w + (int64_t)n0 * ldw, nrec);
+  const uint32_t voff = (uint32_t)((size_t)lc * ldw * 2) + (uint32_t)lk * 16u;
+  const uint16_t* xrow = xsd + (lc < M ? lc : M) * kpitch + lk * 8;
+
+  u32x4_t buf[2][kDenseChunks][2];
+  auto load_stage = [&](u32x4_t (&b)[kDenseChunks][2], int kc) {
+#pragma unroll
+    for (int c = 0; c < kDenseChunks; ++c)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = kc + c * 64 + h * 32;  // first element of this lane group's 32-element block
+        // Past K the lane's offset starts at the end of the resource, which reads as zero.
+        const uint32_t v = (FULL || k + lk * 8 < K) ? voff : nrec;
+        b[c][h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, v, (uint32_t)(k * 2), 0));
+      }
+  };
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  auto compute_stage = [&](const u32x4_t (&b)[kDenseChunks][2], int kc) {
+#pragma unroll
+    for (int c = 0; c < kDenseChunks; ++c)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = kc + c * 64 + h * 32;
+        // K is a multiple of 8, so each lane's 8-element block is wholly inside K
+        // or past it; the LDS rows have 64 elements of slack for the read.
+        u32x4_t a = *reinterpret_cast<const u32x4_t*>(xrow + k);
+        if (!FULL) a = (k + lk * 8 < K) ? a : u32x4_t{0u, 0u, 0u, 0u};
+        acc = mfma16(as_bf16x8(a), as_bf16x8(b[c][h]), acc);
+      }
+  };
+  constexpr int kStage = 64 * kDenseChunks;
+  int kc = 0;
+  load_stage(buf[0], 0);
+  if (kStage < K) load_stage(buf[1], kStage);
+  for (;;) {
+    compute_stage(buf[0], kc);
+    kc += kStage;
+    if (kc >= K) break;
+    if (kc + kStage < K) load_stage(buf[0], kc + kStage);
+    compute_stage(buf[1], kc);
+    kc += kStage;
+    if (kc >= K) break;
+    if (kc + kStage < K) load_stage(buf[1], kc + kStage);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = lk * 4 + r;
+    if (m < M && lc < rows) y[(int64_t)m * ldy + n0 + lc] = f32_to_bf16(acc[r]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Dequantize: out[k, n] = q[k, n] * s[k/g, n] (engine/kernels/quant.py:122-156).
 // With a bf16 output the scale is first rounded to bf16, then the product is
 // rounded to bf16, which is what `dequantize_weight_int4(packed, scale.to(bf16))`
@@ -1278,6 +1374,36 @@ int w4a16_linear(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, 
   if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
   const w4a16_problem q{x, ldx, packed, ldp, scale, lds, y, ldy, M, N, K};
   return w4a16_linear_grouped(&q, 1, group_size, workspace, workspace_bytes, stream);
+}
+
+int w4a16_bf16_gemv(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy, int M, int N,
+                    int K, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
+  if (M > 16) return W4A16_ERR_TOO_LARGE;
+  if (M == 0 || N == 0) return W4A16_OK;
+  if (!y) return W4A16_ERR_NULL;
+  if (K == 0) {
+    hipLaunchKernelGGL(zero_kernel, dim3(ceil_div((int64_t)M * N, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<uint16_t*>(y), ldy, M, N);
+    return launch_status();
+  }
+  if (!x || !w) return W4A16_ERR_NULL;
+  if (ldx < K || ldw < K || ldy < N) return W4A16_ERR_SHAPE;
+  // 16-byte loads: x and w rows 16-byte aligned, K a multiple of 8.
+  if (K % 8 != 0 || ldx % 8 != 0 || ldw % 8 != 0 || !aligned(x, 16) || !aligned(w, 16)) return W4A16_ERR_SHAPE;
+  if ((size_t)16 * ldw * 2 >= 0xffffffffull) return W4A16_ERR_TOO_LARGE;
+  const size_t lds = (size_t)(M + 1) * (K + 72) * 2;
+  if (lds > 160 * 1024) return W4A16_ERR_TOO_LARGE;
+  const int grid = ceil_div(N, 64);
+  const bool full = K % (64 * kDenseChunks) == 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (full)
+    hipLaunchKernelGGL(bf16_gemv_kernel<true>, dim3(grid), dim3(256), lds, s, static_cast<const uint16_t*>(x), ldx,
+                       static_cast<const uint16_t*>(w), ldw, static_cast<uint16_t*>(y), ldy, M, N, K);
+  else
+    hipLaunchKernelGGL(bf16_gemv_kernel<false>, dim3(grid), dim3(256), lds, s, static_cast<const uint16_t*>(x), ldx,
+                       static_cast<const uint16_t*>(w), ldw, static_cast<uint16_t*>(y), ldy, M, N, K);
+  return launch_status();
 }
 
 int w4a16_dequant(const int8_t* packed, int64_t ldp, const float* scale, int64_t lds, void* out, int64_t ldo,

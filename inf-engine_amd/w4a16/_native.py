@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "w4a16_linear_grouped",
     "w4a16_workspace_size_grouped",
     "w4a16_dequant",
+    "w4a16_bf16_gemv",
 )
 
 
@@ -87,6 +88,8 @@ def load_library() -> ctypes.CDLL:
         lib.w4a16_linear.restype = i32
         lib.w4a16_dequant.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
         lib.w4a16_dequant.restype = i32
+        lib.w4a16_bf16_gemv.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, vp]
+        lib.w4a16_bf16_gemv.restype = i32
         pp = ctypes.POINTER(Problem)
         lib.w4a16_linear_grouped.argtypes = [pp, i32, i32, vp, sz, vp]
         lib.w4a16_linear_grouped.restype = i32
@@ -207,6 +210,23 @@ def linear_grouped(xs, weights, group_size: int) -> list[torch.Tensor]:
                                   stream)
     check(rc, "w4a16_linear_grouped")
     return outs
+
+
+def bf16_gemv(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """y = x @ w.T on the current HIP stream; x [M, K] bf16 (M <= 16), w [N, K] bf16."""
+    lib = load_library()
+    m, k = x.shape
+    n = w.shape[0]
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    if w.stride(1) != 1:
+        w = w.contiguous()
+    y = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    rc = lib.w4a16_bf16_gemv(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(), y.stride(0),
+                             m, n, k, stream)
+    check(rc, "w4a16_bf16_gemv")
+    return y
 
 
 def dequant(packed: torch.Tensor, scale: torch.Tensor, group_size: int, out_dtype: torch.dtype) -> torch.Tensor:

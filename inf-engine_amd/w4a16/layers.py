@@ -15,3 +15,25 @@ def linear(x: torch.Tensor, weight) -> torch.Tensor:
     if hasattr(weight, "fused_linear"):
         return weight.fused_linear(x)
     return x @ weight.T
+
+
+def lm_head(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """Logits ``x @ weight.T`` for a dense bf16 ``weight[vocab, d_model]`` (engine/llama_model.py:148).
+
+    Decode-sized inputs (at most 16 rows after flattening the leading
+    dimensions) run the HBM-bound bf16 GEMV kernel of ``libw4a16.so``; larger
+    inputs, where the product is a plain GEMM, use torch's library GEMM.
+    Device tensors only.
+    """
+    from . import _native
+
+    if not x.is_cuda or not weight.is_cuda:
+        raise TypeError("w4a16.lm_head runs only on HIP device tensors")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError(f"lm_head expects bf16 activations and weight, got {x.dtype} and {weight.dtype}")
+    lead = x.shape[:-1]
+    a = x.reshape(-1, x.shape[-1])
+    if a.shape[0] > 16:
+        return (a @ weight.T).reshape(*lead, weight.shape[0])
+    with torch.cuda.device(a.device):
+        return _native.bf16_gemv(a, weight).reshape(*lead, weight.shape[0])

@@ -441,3 +441,57 @@ def test_config4_qwen3_8b_prefill(name, k, n):
                                         ("gate", 4096, 5120, 25600), ("down", 4096, 25600, 5120)])
 def test_config5_qwen3_32b(name, m, k, n):
     full_size_check(m, k, n, seed=m + k + n, label=f"qwen3-32b {name} M={m}")
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 8, 1), (1, 64, 15), (2, 256, 16), (7, 1000, 100), (16, 4096, 1000),
+                                   (1, 4096, 4099), (3, 520, 64)])
+def test_lm_head_bf16_gemv(m, k, n):
+    """Dense bf16 decode GEMV (logits = x @ lm_head.T) against float64."""
+    from w4a16 import lm_head
+
+    say(f"lm_head m={m} k={k} n={n}")
+    g = torch.Generator().manual_seed(m * 7 + k + n)
+    x = torch.randn(m, k, generator=g).bfloat16()
+    w = (torch.randn(n, k, generator=g) * 0.02).bfloat16()
+    y = lm_head(x.to(DEV), w.to(DEV))
+    assert y.shape == (m, n) and y.dtype == torch.bfloat16
+    ref = x.double().numpy() @ w.double().numpy().T
+    check_tolerance(y, ref, f"lm_head {m}x{k}x{n}")
+
+
+def test_lm_head_shapes_and_errors():
+    from w4a16 import _native, lm_head
+
+    say("lm_head shapes and errors")
+    x = torch.randn(2, 3, 256).bfloat16().to(DEV)
+    w = (torch.randn(512, 256) * 0.02).bfloat16().to(DEV)
+    y = lm_head(x, w)
+    assert y.shape == (2, 3, 512)
+    check_tolerance(y.reshape(6, 512), x.reshape(6, 256).double().cpu().numpy() @ w.double().cpu().numpy().T, "3d")
+    big = torch.randn(40, 256).bfloat16().to(DEV)  # M > 16: library GEMM
+    assert torch.equal(lm_head(big, w), big @ w.T)
+    with pytest.raises(ValueError):
+        _native.bf16_gemv(torch.randn(1, 12).bfloat16().to(DEV), torch.randn(4, 12).bfloat16().to(DEV))
+    with pytest.raises(TypeError):
+        lm_head(x.cpu(), w.cpu())
+    z = _native.bf16_gemv(torch.empty(1, 0, dtype=torch.bfloat16, device=DEV),
+                          torch.empty(5, 0, dtype=torch.bfloat16, device=DEV))
+    assert torch.equal(z.float().cpu(), torch.zeros(1, 5))
+
+
+def test_lm_head_qwen3_8b_full_size():
+    """The real output projection: vocab 151936 x d_model 4096 (1.24 GB bf16), M = 1."""
+    from w4a16 import lm_head
+
+    say("lm_head full size")
+    g = torch.Generator(device=DEV).manual_seed(5)
+    w = (torch.randn(151936, 4096, generator=g, device=DEV) * 0.02).bfloat16()
+    x = torch.randn(1, 4096, generator=g, device=DEV).bfloat16()
+    y = lm_head(x, w).float()
+    ref = (x.double() @ w.double().T).float()
+    rms = ref.pow(2).mean().sqrt()
+    _, e = torch.frexp(ref)  # |ref| = f * 2^e with f in [0.5, 1): a bf16 ulp is 2^(e - 8)
+    excess = (y - ref).abs() - torch.ldexp(torch.ones_like(ref), e - 9)
+    assert torch.isfinite(y).all()
+    assert excess.max().item() <= 1e-3 * rms.item()
+    del w
