@@ -71,7 +71,7 @@ struct Launch {
 #define W4A16_MARK(i)                                                                                     \
   do {                                                                                                    \
     if (L.trace && (threadIdx.x & 63) == 0)                                                               \
-      L.trace[((size_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * 8 + (i)] =                  \
+      L.trace[(((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6)) * 8 + (i)] = \
           __builtin_amdgcn_s_memrealtime();                                                               \
   } while (0)
 #else
@@ -149,13 +149,17 @@ __device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split
 //   acc = -136 * sum_k x   (4 MFMAs against a constant -136 operand),
 //   acc += x . (q + 136)   (4 K steps x CPL MFMAs),   total += acc * scale.
 //
-// Workgroup = 4 waves on one strip; blockIdx selects (problem, split, strip)
-// and each wave takes one of the split's gps (=4) groups.  The register budget
-// (one group in flight per wave, buffer loads with scalar row offsets) allows
-// 3 workgroups per CU, so decode-sized grids are resident in a single round.
-// A wave first issues its group's weight and scale loads, then the workgroup
-// copies its activations x[0:M, krange] into LDS, and A fragments are read
-// from LDS at the step that needs them.
+// Workgroup = WAVES waves on one strip; blockIdx selects (problem, split,
+// strip) and wave w takes group split*gps + w of the split's gps (= WAVES)
+// groups.  Every wave issues all of its memory traffic before any arithmetic,
+// in the order it is consumed: its activation fragments (lanes l%16 < M load
+// row l%16 straight from global memory, the rest hold zeros), the group's
+// scales, then the 16 weight loads.  A scheduling barrier keeps the compiler
+// from sinking loads below the MFMAs, so a wave's loads are all in flight
+// together and the waits that follow are partial (vmcnt counts down while the
+// first K steps are already being multiplied).  Waves are then reduced
+// through LDS; with K split across workgroups, splitk_finish sums the split
+// partials in split order.
 // ---------------------------------------------------------------------------
 template <int CPL>
 struct DecodeSlot {
@@ -197,27 +201,33 @@ __device__ __forceinline__ void decode_group(const DecodeSlot<CPL>& d, const bf1
     for (int r = 0; r < 4; ++r) total[t][r] = __builtin_fmaf(acc[t][r], d.s[t], total[t][r]);
 }
 
-// xs: LDS activations [M][kpitch] bf16; g_local = group index within the staged K range.
-template <int CPL>
-__device__ __forceinline__ void decode_compute(const DecodeSlot<CPL>& d, const uint16_t* xs, int kpitch, int g_local,
-                                               int xrow_idx, int lk, f32x4_t (&total)[CPL]) {
-  const uint16_t* xrow = xs + xrow_idx * kpitch + g_local * kGroup + lk * 8;
-  bf16x8_t A[4];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) A[st] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(xrow + st * 32));
-  decode_group<CPL>(d, A, total);
-}
-
-template <int CPL, bool FULL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) void gemv_kernel(Launch L) {
+// MULTI: the launch holds several problems.  A single-problem launch reads its
+// table entry at fixed kernel-argument offsets, so every field arrives with one
+// round of scalar loads instead of two dependent ones.  M1: every problem has
+// M == 1 (batch-1 decode); the row loops and reductions then compile to their
+// one-row form, which measures ~0.4 us faster per launch.
+template <int CPL, int WAVES, bool FULL, bool MULTI, bool M1>
+__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
   constexpr int WCOLS = 16 * CPL;
-  extern __shared__ __attribute__((aligned(16))) float smem[];
+  constexpr int NT = WAVES * 64;
+  extern __shared__ __attribute__((aligned(16))) float smem[];  // [WAVES][M][WCOLS] wave totals
 
-  const int pi = problem_of(L, blockIdx.x);
-  const Problem& P = L.p[pi];
-  const int local = blockIdx.x - P.wg_begin;
-  const int strip = local % P.tiles_n;
-  const int split = local / P.tiles_n;
+  const int pi = MULTI ? problem_of(L, blockIdx.x) : 0;
+  // The empty asm makes the pointer fields live here, so they are fetched in
+  // the same round of scalar loads as the tiling fields instead of after it.
+  const Problem P = L.p[pi];
+  asm volatile("" ::"s"(P.x), "s"(P.packed), "s"(P.scale), "s"(P.ldx), "s"(P.ldp), "s"(P.lds));
+  // Single-problem launches use a (strip, split) grid: no division in the
+  // prologue, which every wave of a CU runs on the shared scalar unit.
+  int strip, split;
+  if constexpr (MULTI) {
+    const uint32_t local = blockIdx.x - (uint32_t)P.wg_begin;
+    strip = (int)(local % (uint32_t)P.tiles_n);
+    split = (int)(local / (uint32_t)P.tiles_n);
+  } else {
+    strip = blockIdx.x;
+    split = blockIdx.y;
+  }
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -225,85 +235,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
   const int lk = lane >> 4;
   const int n0 = strip * WCOLS;
   const int col0 = n0 + lc * CPL;
-  const int M = P.M, N = P.N;
-  const int G = P.K / kGroup;
-  const int g_begin = split * P.gps;
-  const int g_end = min(G, g_begin + P.gps);
-  const int kspan = (g_end - g_begin) * kGroup;
-  const int kpitch = P.gps * kGroup + 8;  // +16 B per row against LDS bank conflicts
+  const int M = M1 ? 1 : P.M, N = P.N;
+  const int G = (uint32_t)P.K / kGroup;
+  const int g = split * P.gps + wave;
+  const bool active = wave < P.gps && g < G;  // wave-uniform
   W4A16_MARK(0);
 
-  // Weight + scale loads for this wave's group.  FULL launches use buffer loads
-  // whose per-lane offset (column, k-block row) is fixed and whose row is a
-  // scalar offset, so no per-load address arithmetic is needed.
-  int g = g_begin + wave;
-  DecodeSlot<CPL> slot;
-  const uint32_t ldp = (uint32_t)P.ldp;
-  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(P.packed, (uint32_t)((size_t)(P.K / 2) * P.ldp));
-  const __amdgpu_buffer_rsrc_t srs = make_rsrc(P.scale, (uint32_t)((size_t)G * P.lds * 4));
-  const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
-  const uint32_t svoff = (uint32_t)col0 * 4u;
-  auto load_group = [&](int gg) {
-    DecodeSlot<CPL>& cur = slot;
-    if constexpr (FULL) {
-      const uint32_t gbase = (uint32_t)gg * kPackedRowsPerGroup * ldp;
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          buffer_load_bytes<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, cur.raw[st][r]);
-      const uint32_t soff = (uint32_t)gg * (uint32_t)P.lds * 4u;
-#pragma unroll
-      for (int t = 0; t < CPL; t += 4) {
-        const f32x4_t v =
-            __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, svoff + 4u * t, soff, 0));
-        cur.s[t] = v[0]; cur.s[t + 1] = v[1]; cur.s[t + 2] = v[2]; cur.s[t + 3] = v[3];
-      }
-    } else {
-      const uint8_t* base = P.packed + (int64_t)gg * kPackedRowsPerGroup * P.ldp;
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          load_packed<CPL, false>(base + (int64_t)(st * 16 + lk * 4 + r) * P.ldp, col0, N, (P.vec & 1) != 0,
-                                  cur.raw[st][r]);
-      load_scales<CPL, false>(P.scale + (int64_t)gg * P.lds, col0, N, (P.vec & 1) != 0, cur.s);
-    }
-  };
-  if (g < g_end) load_group(g);
-  W4A16_MARK(1);
-
-  // Activations of the workgroup's K range -> LDS.
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-  {
-    const bool vec_x = (P.vec & 2) != 0;
-    const int chunks = kspan / 8;
-    for (int i = threadIdx.x; i < M * chunks; i += 256) {
-      const int m = i / chunks, c = i % chunks;
-      const uint16_t* src = P.x + (int64_t)m * P.ldx + (int64_t)g_begin * kGroup + c * 8;
-      *reinterpret_cast<u32x4_t*>(xs + m * kpitch + c * 8) = __builtin_bit_cast(u32x4_t, load_x8(src, vec_x));
-    }
-    if (M < 16)
-      for (int c = threadIdx.x; c < chunks; c += 256)
-        *reinterpret_cast<u32x4_t*>(xs + M * kpitch + c * 8) = u32x4_t{0u, 0u, 0u, 0u};
-  }
-  __syncthreads();
-  W4A16_MARK(2);
-
-  // Lanes of rows past M read the zero row M.
-  const int xrow_idx = lc < M ? lc : M;
   f32x4_t total[CPL];
 #pragma unroll
   for (int t = 0; t < CPL; ++t) total[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  while (g < g_end) {
-    decode_compute<CPL>(slot, xs, kpitch, g - g_begin, xrow_idx, lk, total);
-    g += 4;
-    if (g < g_end) load_group(g);
+  if (active) {
+    // Activation fragments: lane (lc, lk) holds x[lc, g*128 + 32*st + 8*lk .. +8].
+    // FULL launches load them unconditionally (lanes past M read row 0) and
+    // zero them with a select, so no branch or wait sits before the weight loads.
+    bf16x8_t A[4];
+    const uint32_t keep = lc < M ? 0xffffffffu : 0u;
+    DecodeSlot<CPL> d;
+    if constexpr (FULL) {
+      const __amdgpu_buffer_rsrc_t xrs = make_rsrc(P.x, (uint32_t)((size_t)P.ldx * 2 * M));
+      const uint32_t xoff = ((uint32_t)(lc < M ? lc : 0) * (uint32_t)P.ldx + (uint32_t)(g * kGroup + lk * 8)) * 2u;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + st * 64, 0, 0));
+        A[st] = as_bf16x8(v & keep);
+      }
+    } else {
+      const bool vec_x = (P.vec & 2) != 0;
+      const uint16_t* xrow = P.x + (int64_t)(lc < M ? lc : 0) * P.ldx + (int64_t)g * kGroup + lk * 8;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) A[st] = as_bf16x8(__builtin_bit_cast(u32x4_t, load_x8(xrow + st * 32, vec_x)) & keep);
+    }
+    if constexpr (FULL) {
+      const uint32_t ldp = (uint32_t)P.ldp;
+      const __amdgpu_buffer_rsrc_t wrs = make_rsrc(P.packed, (uint32_t)((size_t)(P.K / 2) * P.ldp));
+      const __amdgpu_buffer_rsrc_t srs = make_rsrc(P.scale, (uint32_t)((size_t)G * P.lds * 4));
+      const uint32_t soff = (uint32_t)g * (uint32_t)P.lds * 4u;
+#pragma unroll
+      for (int t = 0; t < CPL; t += 4) {
+        const f32x4_t v = __builtin_bit_cast(
+            f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, (uint32_t)(col0 + t) * 4u, soff, 0));
+        d.s[t] = v[0]; d.s[t + 1] = v[1]; d.s[t + 2] = v[2]; d.s[t + 3] = v[3];
+      }
+      const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
+      const uint32_t gbase = (uint32_t)g * kPackedRowsPerGroup * ldp;
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          buffer_load_bytes<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, d.raw[st][r]);
+    } else {
+      const bool vw = (P.vec & 1) != 0;
+      load_scales<CPL, false>(P.scale + (int64_t)g * P.lds, col0, N, vw, d.s);
+      const uint8_t* base = P.packed + (int64_t)g * kPackedRowsPerGroup * P.ldp;
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          load_packed<CPL, false>(base + (int64_t)(st * 16 + lk * 4 + r) * P.ldp, col0, N, vw, d.raw[st][r]);
+    }
+    // Everything above is in flight before the first MFMA below.
+    __builtin_amdgcn_sched_barrier(0);
+    W4A16_MARK(1);
+    decode_group<CPL>(d, A, total);
   }
   W4A16_MARK(3);
 
-  // Reduce the 4 waves through LDS (reusing the activation buffer).
-  __syncthreads();
+  // Reduce the waves through LDS.  Rows m = 4*lk + r of the MFMA output.
   float* red = smem;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -319,17 +316,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) voi
   W4A16_MARK(4);
   const int elems = M * WCOLS;
   auto wave_sum = [&](int e) {
-    return ((red[e] + red[(size_t)elems + e]) + red[(size_t)2 * elems + e]) + red[(size_t)3 * elems + e];
+    float v = red[e];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) v += red[(size_t)w * elems + e];
+    return v;
   };
   if (P.nsplit == 1) {
-    for (int e = threadIdx.x; e < elems; e += 256) {
+    for (int e = threadIdx.x; e < elems; e += NT) {
       const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
       if (n < N) P.y[(int64_t)m * P.ldy + n] = f32_to_bf16(wave_sum(e));
     }
     W4A16_MARK(5);
     return;
   }
-  splitk_finish<256>(P, M, split, strip, n0, WCOLS, M, wave_sum);
+  splitk_finish<NT>(P, M, split, strip, n0, WCOLS, M, wave_sum);
   W4A16_MARK(6);
 }
 
@@ -978,6 +978,7 @@ int env_int(const char* name, int dflt) {
 struct Plan {
   Kind kind;
   int cpl;
+  int waves;           // gemv: waves per workgroup (4 or 8)
   bool full;           // every problem takes the unconditional (aligned, full tile) load path
   size_t lds_bytes;    // dynamic LDS (gemv / skinny)
   size_t ws_bytes;
@@ -1048,6 +1049,16 @@ Plan make_plan(const w4a16_problem* probs, int count) {
     }
     pl.cpl = cpl;
     const int wcols = 16 * cpl;
+    // Decode: 4 waves per workgroup, or 8 when that would split K more than
+    // 12 ways (K > 6144): the finishing workgroup reads every split's partial,
+    // so long K is better reduced inside the workgroup.
+    int max_g = 0, max_m = 0;
+    for (int i = 0; i < count; ++i) {
+      max_g = std::max(max_g, probs[i].K / kGroup);
+      max_m = std::max(max_m, probs[i].M);
+    }
+    pl.waves = (pl.kind == kGemv && ceil_div(max_g, 4) > 12 && max_m <= 8) ? 8 : 4;
+    pl.waves = env_int("W4A16_WAVES", pl.waves);
     int wg = 0;
     size_t lds = 0;
     for (int i = 0; i < count; ++i) {
@@ -1057,10 +1068,9 @@ Plan make_plan(const w4a16_problem* probs, int count) {
       P.tiles_m = 1;
       P.tiles_n = ceil_div(P.N, wcols);
       if (pl.kind == kGemv) {
-        P.gps = env_int("W4A16_GPS", 4);
+        P.gps = pl.waves;  // one 128-row group per wave
         P.nsplit = ceil_div(G, P.gps);
-        lds = std::max(lds, (size_t)(M + 1) * (P.gps * kGroup + 8) * 2);
-        lds = std::max(lds, (size_t)4 * M * wcols * 4);
+        lds = std::max(lds, (size_t)pl.waves * M * wcols * 4);
       } else {
         // Split K until ~2 workgroups per CU, keeping at least one group per
         // wave and the fp32 partial traffic within a quarter of the weights.
@@ -1075,7 +1085,9 @@ Plan make_plan(const w4a16_problem* probs, int count) {
       P.wg_begin = wg;
       wg += P.tiles_n * P.nsplit;
       const size_t wbytes = (size_t)(P.K / 2) * P.ldp, sbytes = (size_t)G * P.lds * 4;
+      const size_t xbytes = (size_t)P.ldx * 2 * M;
       full = full && (P.vec & 1) && P.N % wcols == 0 && wbytes < 0xffffffffull && sbytes < 0xffffffffull;
+      if (pl.kind == kGemv) full = full && (P.vec & 2) && xbytes < 0xffffffffull;
       if (P.nsplit > 1) {
         pl.counter_off[i] = counters;
         counters += P.tiles_n;
@@ -1166,12 +1178,32 @@ int launch_status() {
   return e == hipSuccess ? W4A16_OK : W4A16_ERR_LAUNCH;
 }
 
-template <int CPL>
-int launch_gemv(const Plan& pl, hipStream_t s) {
+template <int CPL, int WAVES, bool MULTI, bool M1>
+void launch_gemv_as(const Plan& pl, dim3 grid, hipStream_t s) {
+  const dim3 block(WAVES * 64);
   if (pl.full)
-    hipLaunchKernelGGL((gemv_kernel<CPL, true>), dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
+    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, true, MULTI, M1>), grid, block, pl.lds_bytes, s, pl.L);
   else
-    hipLaunchKernelGGL((gemv_kernel<CPL, false>), dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
+    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, false, MULTI, false>), grid, block, pl.lds_bytes, s, pl.L);
+}
+
+template <int CPL, int WAVES>
+int launch_gemv(const Plan& pl, hipStream_t s) {
+  bool m1 = pl.full;
+  for (int i = 0; i < pl.L.count; ++i) m1 = m1 && pl.L.p[i].M == 1;
+  if (pl.L.count > 1) {
+    const dim3 grid(pl.total_wgs);
+    if (m1)
+      launch_gemv_as<CPL, WAVES, true, true>(pl, grid, s);
+    else
+      launch_gemv_as<CPL, WAVES, true, false>(pl, grid, s);
+  } else {
+    const dim3 grid(pl.L.p[0].tiles_n, pl.L.p[0].nsplit);
+    if (m1)
+      launch_gemv_as<CPL, WAVES, false, true>(pl, grid, s);
+    else
+      launch_gemv_as<CPL, WAVES, false, false>(pl, grid, s);
+  }
   return launch_status();
 }
 
@@ -1235,7 +1267,10 @@ int launch_plan(const w4a16_problem* probs, int count, void* workspace, size_t w
   if (pl.too_many_counters) return W4A16_ERR_TOO_LARGE;
   if (pl.ws_bytes > 0 && (!workspace || workspace_bytes < pl.ws_bytes)) return W4A16_ERR_WORKSPACE;
   bind(pl, workspace);
-  if (pl.kind == kGemv) return pl.cpl == 4 ? launch_gemv<4>(pl, s) : launch_gemv<8>(pl, s);
+  if (pl.kind == kGemv) {
+    if (pl.waves == 8) return pl.cpl == 4 ? launch_gemv<4, 8>(pl, s) : launch_gemv<8, 8>(pl, s);
+    return pl.cpl == 4 ? launch_gemv<4, 4>(pl, s) : launch_gemv<8, 4>(pl, s);
+  }
   if (pl.kind == kSkinny) {
     if (pl.full)
       hipLaunchKernelGGL(skinny_kernel<true>, dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
