@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 3
+#define W4A16_ABI_VERSION 4
 
 /* Most problems one grouped call accepts. */
 #define W4A16_MAX_PROBLEMS 16
@@ -39,7 +39,7 @@ extern "C" {
 #define W4A16_ERR_WORKSPACE 5   /* workspace NULL or smaller than w4a16_workspace_size() */
 #define W4A16_ERR_LAUNCH 6      /* a HIP launch reported an error */
 #define W4A16_ERR_DTYPE 7       /* unknown dtype code */
-#define W4A16_ERR_TOO_LARGE 8   /* more split-K strips / tiles than the 16,384 workspace counters */
+#define W4A16_ERR_TOO_LARGE 8   /* problem exceeds what the entry point supports (w4a16_bf16_gemv: M > 16) */
 
 /* dtype codes for w4a16_dequant. */
 #define W4A16_DTYPE_F32 0
@@ -72,12 +72,15 @@ const char* w4a16_error_string(int code);
 
 /*
  * Bytes of device workspace w4a16_linear needs for an (M, N, K) call; 0 means
- * the call needs none.  The first 64 KiB of a workspace are split-K arrival
- * counters: they must be zero before the first call that uses the buffer and
- * are left at zero by every completed call, so a buffer is zeroed once when it
- * is allocated.  Calls that share a workspace must be ordered (same stream).
- * Replaces no reference entry point: the reference kernel needs no workspace
- * (engine/kernels/quant.py:270-280 allocates only the output).
+ * the call needs none.  A workspace of W bytes is used in two halves: the
+ * lower half holds the decode kernels' split-K partial slots, which must be
+ * zero before the first call that uses the buffer and are left at zero by
+ * every completed call; the upper half is GEMM scratch.  So: zero a buffer
+ * once when it is allocated, pass its full size on every call, and replace it
+ * by a new zeroed buffer to grow it.  Calls that share a workspace must be
+ * ordered (same stream).  Replaces no reference entry point: the reference
+ * kernel needs no workspace (engine/kernels/quant.py:270-280 allocates only
+ * the output).
  */
 int w4a16_workspace_size(int M, int N, int K, int group_size, size_t* bytes);
 

@@ -32,8 +32,7 @@ using namespace w4a16;
 namespace {
 
 constexpr int kMaxProblems = W4A16_MAX_PROBLEMS;
-constexpr int kCounterBytes = 65536;           // split-K arrival counters at the head of the workspace
-constexpr int kMaxCounters = kCounterBytes / 4;
+constexpr uint32_t kSpinLimit = 1u << 20;      // polls before a finishing workgroup gives up (writes NaN)
 
 // One projection of a launch, as the device sees it.
 struct Problem {
@@ -45,8 +44,8 @@ struct Problem {
   int64_t lds;
   uint16_t* y;         // bf16 [M, N], row stride ldy elements
   int64_t ldy;
-  float* part;         // split-K partials [nsplit][M][N] (workspace)
-  uint32_t* counters;  // one arrival counter per strip / tile (workspace, zero between calls)
+  float* part;         // gemm: split-K partials [nsplit][M][N]; gemv / skinny: published
+                       // partial slots [nsplit - 1][M][N] (workspace, zero between calls)
   float* rowsum;       // gemm: 136 * row sums [K/128][M] (workspace, maybe shared)
   int M, N, K;
   int wg_begin;        // first workgroup of this problem in the launch grid
@@ -89,52 +88,111 @@ __device__ __forceinline__ int problem_of(const Launch& L, int wg) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-K finish shared by the M <= 32 kernels.  Each workgroup publishes its
-// fp32 partial for (split, strip) with agent-coherent stores (no whole-L2
-// writeback / invalidate, which an agent-scope release/acquire fence costs on
-// this chip).  Every wave waits for its stores to be acknowledged before the
-// barrier, so when thread 0 bumps the strip's arrival counter all partials of
-// the workgroup are visible device-wide.  The last arrival, whose counter
-// update has returned before it issues any load, sums the partials in split
-// order (deterministic), writes bf16 and resets the counter to zero.  Partials
-// are loaded 8 at a time so their latencies overlap.
+// Split-K reduction shared by the M <= 32 kernels, without atomics.
+//
+// The workgroup of the last split (split == nsplit - 1) of a strip finishes
+// it; the others publish their fp32 partial and exit.  A published slot holds
+// the bitwise complement of the partial, so a slot reading 0 is still empty
+// (the one partial whose complement is 0, the NaN 0xFFFFFFFF, is published as
+// the canonical NaN 0x7FC00000).  The finisher polls the nsplit - 1 slots of
+// each of its elements with agent-coherent loads, sums them in split order
+// with its own partial last (deterministic), writes bf16 and zeroes the slots
+// again, so the slots are empty at the start of every call.
+//
+// Why no workgroup can wait forever: the grid orders workgroups split-major
+// ((strip, split) grids, or split-major ids within a problem), so a finisher
+// is dispatched after every workgroup it waits for, and those never wait on
+// anything.  The poll is still bounded (kSpinLimit); a finisher that gives up
+// writes NaN, so a failure is visible rather than a hang.
+//
+// An arrival counter instead (one agent-scope atomic per workgroup, the last
+// arrival reduces) measures 1 us (8 splits) to 3.3 us (24 splits) slower per
+// launch on MI355X: atomics on one address serialize.
 // ---------------------------------------------------------------------------
-template <int NT, class PartialFn>
-__device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split, int strip, int n0, int wcols,
-                                              int rows, PartialFn partial) {
+__device__ __forceinline__ uint32_t publish_bits(float v) {
+  uint32_t b = __float_as_uint(v);
+  if (b == 0xffffffffu) b = 0x7fc00000u;
+  return ~b;
+}
+
+// EPT: most elements (rows x columns of the strip) one thread handles.  The
+// finisher keeps all of a thread's polls for a chunk of splits in flight at
+// once, so a thread with several elements waits about one round trip per
+// chunk rather than one per element.
+template <int NT, int EPT, class PartialFn>
+__device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split, int n0, int wcols, int rows,
+                                              PartialFn partial) {
+  constexpr int SCH = EPT >= 8 ? 2 : (EPT >= 4 ? 4 : 8);  // splits per chunk: EPT * SCH polls in flight
   const int N = P.N;
   const int elems = rows * wcols;
-  float* part = P.part + (size_t)split * M * N;
-  for (int e = threadIdx.x; e < elems; e += NT) {
-    const int m = e / wcols, c = e % wcols, n = n0 + c;
-    if (n < N) store_coherent(part + (size_t)m * N + n, partial(e));
-  }
-  wait_vmem();
-  __syncthreads();
-  __shared__ int is_last;
-  if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(P.counters + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (prev == (uint32_t)(P.nsplit - 1));
-  }
-  __syncthreads();
-  if (!is_last) return;
-  for (int e = threadIdx.x; e < elems; e += NT) {
-    const int m = e / wcols, c = e % wcols, n = n0 + c;
-    if (n < N) {
-      const float* src = P.part + (size_t)m * N + n;
-      const size_t stride = (size_t)M * N;
-      float v = 0.f;
-      for (int sp0 = 0; sp0 < P.nsplit; sp0 += 8) {
-        float t[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = sp0 + i < P.nsplit ? load_coherent(src + (size_t)(sp0 + i) * stride) : 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v += t[i];
-      }
-      P.y[(int64_t)m * P.ldy + n] = f32_to_bf16(v);
+  const size_t stride = (size_t)M * N;
+  uint32_t* slots = reinterpret_cast<uint32_t*>(P.part);
+  const int last = P.nsplit - 1;
+  if (split != last) {
+    uint32_t* dst = slots + (size_t)split * stride;
+    for (int e = threadIdx.x; e < elems; e += NT) {
+      const int m = e / wcols, c = e % wcols, n = n0 + c;
+      if (n < N) __hip_atomic_store(dst + (size_t)m * N + n, publish_bits(partial(e)), __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
     }
+    return;
   }
-  if (threadIdx.x == 0) __hip_atomic_store(P.counters + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  size_t off[EPT];
+  bool ok[EPT];
+  float own[EPT], v[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = threadIdx.x + j * NT;
+    const int m = e / wcols, c = e % wcols, n = n0 + c;
+    ok[j] = e < elems && n < N;
+    off[j] = ok[j] ? (size_t)m * N + n : 0;
+    own[j] = ok[j] ? partial(e) : 0.f;
+    v[j] = 0.f;
+  }
+  bool timed_out = false;
+  for (int sp0 = 0; sp0 < last; sp0 += SCH) {
+    uint32_t t[EPT][SCH];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+#pragma unroll
+      for (int i = 0; i < SCH; ++i)
+        t[j][i] = ok[j] && sp0 + i < last ? __hip_atomic_load(slots + (size_t)(sp0 + i) * stride + off[j],
+                                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                          : 1u;
+    for (uint32_t spins = 0;; ++spins) {
+      bool missing = false;
+#pragma unroll
+      for (int j = 0; j < EPT; ++j)
+#pragma unroll
+        for (int i = 0; i < SCH; ++i) missing = missing || t[j][i] == 0u;
+      if (!missing) break;
+      if (spins == kSpinLimit) {
+        timed_out = true;
+        break;
+      }
+#pragma unroll
+      for (int j = 0; j < EPT; ++j)
+#pragma unroll
+        for (int i = 0; i < SCH; ++i)
+          if (t[j][i] == 0u)
+            t[j][i] = __hip_atomic_load(slots + (size_t)(sp0 + i) * stride + off[j], __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+#pragma unroll
+      for (int i = 0; i < SCH; ++i)
+        if (sp0 + i < last) v[j] += __uint_as_float(~t[j][i]);
+  }
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    if (!ok[j]) continue;
+    const int e = threadIdx.x + j * NT;
+    const int m = e / wcols, n = n0 + e % wcols;
+    P.y[(int64_t)m * P.ldy + n] = timed_out ? (uint16_t)0x7fc0 : f32_to_bf16(v[j] + own[j]);
+    for (int sp = 0; sp < last; ++sp)
+      __hip_atomic_store(slots + (size_t)sp * stride + off[j], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -203,10 +261,12 @@ __device__ __forceinline__ void decode_group(const DecodeSlot<CPL>& d, const bf1
 
 // MULTI: the launch holds several problems.  A single-problem launch reads its
 // table entry at fixed kernel-argument offsets, so every field arrives with one
-// round of scalar loads instead of two dependent ones.  M1: every problem has
-// M == 1 (batch-1 decode); the row loops and reductions then compile to their
-// one-row form, which measures ~0.4 us faster per launch.
-template <int CPL, int WAVES, bool FULL, bool MULTI, bool M1>
+// round of scalar loads instead of two dependent ones.  MROWS (1, 4, 8 or 16)
+// bounds M for every problem of the launch.  MROWS == 1 (batch-1 decode)
+// compiles the row loops and reductions to their one-row form, which measures
+// ~0.4 us faster per launch; the bound also sizes the split-K finisher's
+// per-thread polls (splitk_finish).
+template <int CPL, int WAVES, bool FULL, bool MULTI, int MROWS>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
   constexpr int WCOLS = 16 * CPL;
   constexpr int NT = WAVES * 64;
@@ -235,7 +295,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
   const int lk = lane >> 4;
   const int n0 = strip * WCOLS;
   const int col0 = n0 + lc * CPL;
-  const int M = M1 ? 1 : P.M, N = P.N;
+  const int M = MROWS == 1 ? 1 : P.M, N = P.N;
   const int G = (uint32_t)P.K / kGroup;
   const int g = split * P.gps + wave;
   const bool active = wave < P.gps && g < G;  // wave-uniform
@@ -329,7 +389,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
     W4A16_MARK(5);
     return;
   }
-  splitk_finish<NT>(P, M, split, strip, n0, WCOLS, M, wave_sum);
+  splitk_finish<NT, (MROWS * WCOLS + NT - 1) / NT>(P, M, split, n0, WCOLS, M, wave_sum);
   W4A16_MARK(6);
 }
 
@@ -464,7 +524,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(Launch L) {
     }
     return;
   }
-  splitk_finish<256>(P, M, split, strip, n0, WCOLS, M, wave_sum);
+  splitk_finish<256, 32 * WCOLS / 256>(P, M, split, n0, WCOLS, M, wave_sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -981,14 +1041,12 @@ struct Plan {
   int waves;           // gemv: waves per workgroup (4 or 8)
   bool full;           // every problem takes the unconditional (aligned, full tile) load path
   size_t lds_bytes;    // dynamic LDS (gemv / skinny)
-  size_t ws_bytes;
+  size_t ws_bytes;     // bytes of the plan's workspace half (see bind())
   int total_wgs;
   int rs_wgs;          // rowsum_kernel workgroups
   int red_wgs;         // splitk_reduce_kernel workgroups (gemm with split K)
-  bool too_many_counters;
   Launch L;            // device table (workspace pointers filled in by bind())
   size_t part_off[kMaxProblems], rowsum_off[kMaxProblems];
-  int counter_off[kMaxProblems];
   int rowsum_src[kMaxProblems];  // problem whose row sums this one uses
 };
 
@@ -1038,8 +1096,7 @@ Plan make_plan(const w4a16_problem* probs, int count) {
     pl.rowsum_src[i] = i;
   }
 
-  int counters = 0;
-  size_t ws = kCounterBytes;
+  size_t ws = 0;
   if (pl.kind == kGemv || pl.kind == kSkinny) {
     int cpl = pl.kind == kSkinny ? kSkinnyCPL : env_int("W4A16_CPL", 8);
     if (pl.kind == kGemv && cpl == 8) {
@@ -1089,10 +1146,8 @@ Plan make_plan(const w4a16_problem* probs, int count) {
       full = full && (P.vec & 1) && P.N % wcols == 0 && wbytes < 0xffffffffull && sbytes < 0xffffffffull;
       if (pl.kind == kGemv) full = full && (P.vec & 2) && xbytes < 0xffffffffull;
       if (P.nsplit > 1) {
-        pl.counter_off[i] = counters;
-        counters += P.tiles_n;
         pl.part_off[i] = ws;
-        ws = align256(ws + (size_t)P.nsplit * M * P.N * 4);
+        ws = align256(ws + (size_t)(P.nsplit - 1) * M * P.N * 4);
       }
     }
     pl.lds_bytes = lds;
@@ -1151,21 +1206,27 @@ Plan make_plan(const w4a16_problem* probs, int count) {
   }
   pl.full = full;
   pl.L.total_wgs = pl.total_wgs;
-  pl.too_many_counters = counters > kMaxCounters;
-  pl.ws_bytes = (counters > 0 || pl.kind == kGemm) ? ws : 0;
+  pl.ws_bytes = ws;
   return pl;
 }
 
-// Point the device table at the workspace.
-void bind(Plan& pl, void* workspace) {
+// Point the device table at the workspace.  A workspace of W bytes is split
+// in two halves: the decode kernels' published-partial slots live in the
+// lower half, which is zero between calls (every finisher zeroes what it
+// read), and the GEMM's row sums and split partials in the upper half, which
+// holds garbage after a GEMM.  Keeping them apart is what lets the decode
+// slots rely on "0 = empty" whatever ran before on the same workspace.
+void bind(Plan& pl, void* workspace, size_t workspace_bytes) {
   char* ws = static_cast<char*>(workspace);
+  char* upper = ws + ((workspace_bytes / 2) & ~(size_t)255);
   for (int i = 0; i < pl.L.count; ++i) {
     Problem& P = pl.L.p[i];
-    if (P.nsplit > 1) {
-      if (pl.kind != kGemm) P.counters = reinterpret_cast<uint32_t*>(ws) + pl.counter_off[i];
+    if (pl.kind == kGemm) {
+      if (P.nsplit > 1) P.part = reinterpret_cast<float*>(upper + pl.part_off[i]);
+      P.rowsum = reinterpret_cast<float*>(upper + pl.rowsum_off[pl.rowsum_src[i]]);
+    } else if (P.nsplit > 1) {
       P.part = reinterpret_cast<float*>(ws + pl.part_off[i]);
     }
-    if (pl.kind == kGemm) P.rowsum = reinterpret_cast<float*>(ws + pl.rowsum_off[pl.rowsum_src[i]]);
   }
 #ifdef W4A16_EXP
   pl.L.trace = getenv("W4A16_TRACE") ? reinterpret_cast<uint64_t*>(strtoull(getenv("W4A16_TRACE"), nullptr, 0))
@@ -1173,37 +1234,43 @@ void bind(Plan& pl, void* workspace) {
 #endif
 }
 
+// Workspace bytes a plan needs: twice its half, rounded.
+size_t plan_bytes(const Plan& pl) { return pl.ws_bytes == 0 ? 0 : 2 * align256(pl.ws_bytes) + 256; }
+
 int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? W4A16_OK : W4A16_ERR_LAUNCH;
 }
 
-template <int CPL, int WAVES, bool MULTI, bool M1>
+template <int CPL, int WAVES, bool MULTI, int MROWS>
 void launch_gemv_as(const Plan& pl, dim3 grid, hipStream_t s) {
   const dim3 block(WAVES * 64);
   if (pl.full)
-    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, true, MULTI, M1>), grid, block, pl.lds_bytes, s, pl.L);
+    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, true, MULTI, MROWS>), grid, block, pl.lds_bytes, s, pl.L);
   else
-    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, false, MULTI, false>), grid, block, pl.lds_bytes, s, pl.L);
+    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, false, MULTI, 16>), grid, block, pl.lds_bytes, s, pl.L);
+}
+
+template <int CPL, int WAVES, bool MULTI>
+void launch_gemv_rows(const Plan& pl, dim3 grid, int max_m, hipStream_t s) {
+  if (max_m == 1)
+    launch_gemv_as<CPL, WAVES, MULTI, 1>(pl, grid, s);
+  else if (max_m <= 4)
+    launch_gemv_as<CPL, WAVES, MULTI, 4>(pl, grid, s);
+  else if (max_m <= 8)
+    launch_gemv_as<CPL, WAVES, MULTI, 8>(pl, grid, s);
+  else
+    launch_gemv_as<CPL, WAVES, MULTI, 16>(pl, grid, s);
 }
 
 template <int CPL, int WAVES>
 int launch_gemv(const Plan& pl, hipStream_t s) {
-  bool m1 = pl.full;
-  for (int i = 0; i < pl.L.count; ++i) m1 = m1 && pl.L.p[i].M == 1;
-  if (pl.L.count > 1) {
-    const dim3 grid(pl.total_wgs);
-    if (m1)
-      launch_gemv_as<CPL, WAVES, true, true>(pl, grid, s);
-    else
-      launch_gemv_as<CPL, WAVES, true, false>(pl, grid, s);
-  } else {
-    const dim3 grid(pl.L.p[0].tiles_n, pl.L.p[0].nsplit);
-    if (m1)
-      launch_gemv_as<CPL, WAVES, false, true>(pl, grid, s);
-    else
-      launch_gemv_as<CPL, WAVES, false, false>(pl, grid, s);
-  }
+  int max_m = 0;
+  for (int i = 0; i < pl.L.count; ++i) max_m = std::max(max_m, pl.L.p[i].M);
+  if (pl.L.count > 1)
+    launch_gemv_rows<CPL, WAVES, true>(pl, dim3(pl.total_wgs), max_m, s);
+  else
+    launch_gemv_rows<CPL, WAVES, false>(pl, dim3(pl.L.p[0].tiles_n, pl.L.p[0].nsplit), max_m, s);
   return launch_status();
 }
 
@@ -1264,9 +1331,9 @@ int for_each_chunk(const w4a16_problem& q, Fn fn) {
 // Launch one planned batch (all problems of one kind).
 int launch_plan(const w4a16_problem* probs, int count, void* workspace, size_t workspace_bytes, hipStream_t s) {
   Plan pl = make_plan(probs, count);
-  if (pl.too_many_counters) return W4A16_ERR_TOO_LARGE;
-  if (pl.ws_bytes > 0 && (!workspace || workspace_bytes < pl.ws_bytes)) return W4A16_ERR_WORKSPACE;
-  bind(pl, workspace);
+  const size_t need = plan_bytes(pl);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return W4A16_ERR_WORKSPACE;
+  bind(pl, workspace, workspace_bytes);
   if (pl.kind == kGemv) {
     if (pl.waves == 8) return pl.cpl == 4 ? launch_gemv<4, 8>(pl, s) : launch_gemv<8, 8>(pl, s);
     return pl.cpl == 4 ? launch_gemv<4, 4>(pl, s) : launch_gemv<8, 4>(pl, s);
@@ -1290,8 +1357,7 @@ int launch_plan(const w4a16_problem* probs, int count, void* workspace, size_t w
 // Workspace bytes launch_plan needs for one batch.
 int plan_workspace(const w4a16_problem* probs, int count, size_t* bytes) {
   const Plan pl = make_plan(probs, count);
-  if (pl.too_many_counters) return W4A16_ERR_TOO_LARGE;
-  *bytes = std::max(*bytes, pl.ws_bytes);
+  *bytes = std::max(*bytes, plan_bytes(pl));
   return W4A16_OK;
 }
 

@@ -123,9 +123,9 @@ def workspace_size(m: int, n: int, k: int, group_size: int = 128) -> int:
     return out.value
 
 
-# One zeroed workspace per (device, stream).  The head of a workspace holds
-# split-K arrival counters that every call leaves at zero, so a buffer is only
-# zeroed when it is (re)allocated.  Calls on one stream are ordered, which is
+# One zeroed workspace per (device, stream).  Its lower half holds the decode
+# kernels' split-K partial slots, which every call leaves at zero, so a buffer
+# is only zeroed when it is (re)allocated; the full size is passed on every call.  Calls on one stream are ordered, which is
 # what makes sharing the buffer safe.
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 _ws_lock = threading.Lock()

@@ -224,11 +224,16 @@ def test_fused_linear_reshapes_leading_dims():
     np.testing.assert_array_equal(dense.cpu().numpy(), orc.dequantize(packed.numpy(), scale.numpy()).T)
 
 
-def test_split_k_deterministic_and_counters_reset():
-    """Repeated and interleaved calls sharing one workspace give identical bits."""
+def test_split_k_deterministic_and_slots_reset():
+    """Repeated and interleaved calls sharing one workspace give identical bits.
+
+    The decode calls' published-partial slots must be empty again after every
+    call, whatever ran in between: here a split-K GEMM (M=64) and a skinny call
+    (M=24) use the same workspace between decode calls."""
     from w4a16 import int4_matmul
 
-    probs = [rand_problem(m, k, n, seed=m + k) for (m, k, n) in [(1, 4096, 12288), (4, 12288, 4096), (16, 4096, 1024)]]
+    shapes = [(1, 4096, 12288), (64, 1024, 512), (4, 12288, 4096), (24, 4096, 1024), (16, 4096, 1024), (1, 4096, 1024)]
+    probs = [rand_problem(m, k, n, seed=m + k) for (m, k, n) in shapes]
     first = [int4_matmul(*p) for p in probs]
     for _ in range(3):
         for p, y0 in zip(probs, first):

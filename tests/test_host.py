@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(native_lib):
     assert set(names) == set(_native.EXPORTED_SYMBOLS), names
     for name in names:
         assert hasattr(native_lib, name), name
-    assert native_lib.w4a16_abi_version() == 3
+    assert native_lib.w4a16_abi_version() == 4
 
 
 def _linear(lib, *, x=1, ldx=4096, packed=1, ldp=4096, scale=1, lds=4096, y=1, ldy=4096, m=1, n=4096,
@@ -118,11 +118,15 @@ def test_workspace_planning(native_lib):
     ws = _native.workspace_size
     assert ws(0, 4096, 4096) == 0
     assert ws(1, 0, 4096) == 0
-    # M=1 Qwen3-8B gate: split-K partials (fp32 [splits, 1, N]) after 64 KiB of counters.
-    b = ws(1, 12288, 4096)
-    assert b > 65536 and (b - 65536) % (12288 * 4) == 0
-    # Large M: per-(group, row) correction sums.
-    assert ws(2048, 12288, 4096) == 65536 + 32 * 2048 * 4
+    # A workspace is two halves plus 256 B of alignment slack.
+    def half(b):
+        assert (b - 256) % 512 == 0
+        return (b - 256) // 2
+
+    # M=1 Qwen3-8B gate: 8 K splits, 7 published fp32 partial slots [7, 1, N] in the lower half.
+    assert half(ws(1, 12288, 4096)) == 7 * 12288 * 4
+    # Large M: per-(group, row) correction sums in the upper half.
+    assert half(ws(2048, 12288, 4096)) == 32 * 2048 * 4
     with pytest.raises(AssertionError):
         ws(1, 4096, 4096, 64)
     with pytest.raises(ValueError):
@@ -133,8 +137,8 @@ def test_workspace_planning(native_lib):
             for n in (64, 1000, 1024, 12288):
                 b = ws(m, n, k)
                 if b:
-                    splits = (b - 65536) // (m * n * 4)
-                    assert 2 <= splits <= (k // 128 + 3) // 4
+                    slots = half(b) // (m * n * 4)  # nsplit - 1, rounded down by the 256-B alignment
+                    assert 1 <= slots + (1 if half(b) % (m * n * 4) else 0) <= (k // 128 + 3) // 4
 
 
 def test_int4_matmul_rejects_host_tensors_and_bad_args():
