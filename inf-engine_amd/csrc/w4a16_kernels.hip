@@ -1098,23 +1098,29 @@ Plan make_plan(const w4a16_problem* probs, int count) {
 
   size_t ws = 0;
   if (pl.kind == kGemv || pl.kind == kSkinny) {
-    int cpl = pl.kind == kSkinny ? kSkinnyCPL : env_int("W4A16_CPL", 8);
-    if (pl.kind == kGemv && cpl == 8) {
-      // 64-column strips when a problem is not a multiple of 128 columns.
-      for (int i = 0; i < count; ++i)
-        if (probs[i].N % 128 != 0) cpl = 4;
+    // Decode shape choice (measured over the Qwen3-8B / 32B projections at
+    // M = 1..16 on MI355X):
+    //  * 128-column strips (CPL 8), or 64-column strips (CPL 4) when N is not
+    //    a multiple of 128 or 128-column strips would give the launch fewer
+    //    than 128 workgroups (k/v projections: more, smaller workgroups);
+    //  * 4 waves per workgroup (one 128-row group each), or 8 when M >= 8,
+    //    when 4 would launch more than 1000 workgroups, or split K more than
+    //    20 ways: past that, reducing inside the workgroup beats more splits.
+    int max_m = 0, wg8 = 0, max_split4 = 0, n_odd = 0;
+    for (int i = 0; i < count; ++i) {
+      const int G = probs[i].K / kGroup;
+      max_m = std::max(max_m, probs[i].M);
+      wg8 += ceil_div(probs[i].N, 128) * ceil_div(G, 4);
+      max_split4 = std::max(max_split4, ceil_div(G, 4));
+      n_odd += probs[i].N % 128 != 0;
     }
+    int cpl = kSkinnyCPL;
+    if (pl.kind == kGemv) cpl = env_int("W4A16_CPL", (n_odd > 0 || wg8 < 128) ? 4 : 8);
     pl.cpl = cpl;
     const int wcols = 16 * cpl;
-    // Decode: 4 waves per workgroup, or 8 when that would split K more than
-    // 12 ways (K > 6144): the finishing workgroup reads every split's partial,
-    // so long K is better reduced inside the workgroup.
-    int max_g = 0, max_m = 0;
-    for (int i = 0; i < count; ++i) {
-      max_g = std::max(max_g, probs[i].K / kGroup);
-      max_m = std::max(max_m, probs[i].M);
-    }
-    pl.waves = (pl.kind == kGemv && ceil_div(max_g, 4) > 12 && max_m <= 8) ? 8 : 4;
+    int wg4 = 0;
+    for (int i = 0; i < count; ++i) wg4 += ceil_div(probs[i].N, wcols) * ceil_div(probs[i].K / kGroup, 4);
+    pl.waves = (pl.kind == kGemv && (max_m >= 8 || wg4 > 1000 || max_split4 > 20)) ? 8 : 4;
     pl.waves = env_int("W4A16_WAVES", pl.waves);
     int wg = 0;
     size_t lds = 0;
