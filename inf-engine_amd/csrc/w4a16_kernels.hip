@@ -23,6 +23,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "../../include/w4a16.h"
 #include "w4a16_device.h"
@@ -619,8 +620,17 @@ __device__ __forceinline__ void gemm_unpack(const uint32_t (&raw)[4], bf16x8_t (
 template <int CPL, bool FULL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void gemm_kernel(Launch L) {
   constexpr int WCOLS = 16 * CPL;       // columns per wave
-  __shared__ u32x4_t As[2][4 * kGemmMT * 64];  // [buf][step][subtile][lane] 16 B each
-  __shared__ __attribute__((aligned(16))) float Cs[2][kGemmRows];
+  // Two activation buffers [step][subtile][lane] (16 B each) and two row-sum
+  // buffers, as separate objects so that alias analysis can tell a copy into
+  // one from a read of the other.
+  __shared__ u32x4_t As0[4 * kGemmMT * 64], As1[4 * kGemmMT * 64];
+  __shared__ __attribute__((aligned(16))) float Cs0[kGemmRows], Cs1[kGemmRows];
+  auto a_buf = [&](auto tag) -> u32x4_t* {
+    if constexpr (decltype(tag)::value == 0) return As0; else return As1;
+  };
+  auto c_buf = [&](auto tag) -> float* {
+    if constexpr (decltype(tag)::value == 0) return Cs0; else return Cs1;
+  };
 
   // ---- work assignment ----
   int wid = blockIdx.x;
@@ -660,36 +670,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   const __amdgpu_buffer_rsrc_t srs = make_rsrc(P.scale, (uint32_t)((size_t)G * P.lds * 4));
   const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
   // Activation rows this lane copies (clamped: rows past M compute values that are never stored).
-  const uint16_t* xlane = P.x + (int64_t)(m0 + lc) * P.ldx + (wave * 4 + lk) * 8;
-  const int64_t xstep = (int64_t)16 * P.ldx;     // 16 rows
-  const int last_full = (M - 1 - m0 - lc) / 16;  // subtiles whose row m0 + 16i + lc < M
-  int crow = m0 + (threadIdx.x & 127);
-  crow = crow < M ? crow : M - 1;
-
-  auto stage_a = [&](int g, int b) {
+  // Activations come through a buffer resource based at this tile's first
+  // row, so every copy is one 32-bit per-lane offset plus a scalar group
+  // offset (no 64-bit address arithmetic per copy).  Rows past M are clamped
+  // to the last row: they compute values that are never stored.
+  const int tile_rows = min(kGemmRows, M - m0);
+  const __amdgpu_buffer_rsrc_t xrs =
+      make_rsrc(P.x + (int64_t)m0 * P.ldx, (uint32_t)((size_t)tile_rows * P.ldx * 2));
+  uint32_t xv[kGemmMT];
 #pragma unroll
-    for (int i = 0; i < kGemmMT; ++i) {
-      const int ii = i <= last_full ? i : last_full;
-      const uint16_t* src = xlane + (int64_t)ii * xstep + (int64_t)g * kGroup;
-      __builtin_amdgcn_global_load_lds((const void*)src,
-                                       (void __attribute__((address_space(3)))*)&As[b][(wave * kGemmMT + i) * 64],
-                                       16, 0, 0);
-    }
+  for (int i = 0; i < kGemmMT; ++i) {
+    const int row = min(16 * i + lc, tile_rows - 1);
+    xv[i] = ((uint32_t)row * (uint32_t)P.ldx + (uint32_t)((wave * 4 + lk) * 8)) * 2u;
+  }
+  const __amdgpu_buffer_rsrc_t crs = make_rsrc(P.rowsum, (uint32_t)((size_t)G * M * 4));
+  const uint32_t cv = (uint32_t)min(m0 + (int)(threadIdx.x & 127), M - 1) * 4u;
+
+  auto stage_a = [&](int g, auto buf_tag) {
+    u32x4_t* as = a_buf(buf_tag);
+    float* cs = c_buf(buf_tag);
+#pragma unroll
+    for (int i = 0; i < kGemmMT; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (void __attribute__((address_space(3)))*)&as[(wave * kGemmMT + i) * 64],
+                                               16, xv[i], (uint32_t)g * (kGroup * 2), 0, 0);
     if (wave < 2)
-      __builtin_amdgcn_global_load_lds((const void*)(P.rowsum + (int64_t)g * M + crow),
-                                       (void __attribute__((address_space(3)))*)&Cs[b][wave * 64], 4, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(crs, (void __attribute__((address_space(3)))*)&cs[wave * 64], 4, cv,
+                                               (uint32_t)g * (uint32_t)M * 4u, 0, 0);
   };
-  auto load_b = [&](int g, uint32_t (&raw)[4][4], float (&s)[CPL]) {
+  // Packed weights of K step st of group g: 4 packed rows x CPL bytes per lane.
+  auto load_b_step = [&](int g, int st, uint32_t (&raw)[4]) {
     if constexpr (FULL) {
       const uint32_t gbase = (uint32_t)g * kPackedRowsPerGroup * ldp;
 #pragma unroll
-      for (int st = 0; st < 4; ++st)
+      for (int r = 0; r < 4; ++r) {
+        uint32_t w[1];
+        buffer_load_bytes<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, w);
+        raw[r] = w[0];
+      }
+    } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          uint32_t w[1];
-          buffer_load_bytes<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, w);
-          raw[st][r] = w[0];
-        }
+      for (int r = 0; r < 4; ++r) {
+        const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
+        uint32_t w[1];
+        load_packed<CPL, false>(P.packed + pr * P.ldp, col0, N, (P.vec & 1) != 0, w);
+        raw[r] = w[0];
+      }
+    }
+  };
+  auto load_scales_b = [&](int g, float (&s)[CPL]) {
+    if constexpr (FULL) {
       const uint32_t soff = (uint32_t)g * (uint32_t)P.lds * 4u;
       if constexpr (CPL == 4) {
         const f32x4_t v =
@@ -701,17 +730,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         s[0] = v[0]; s[1] = v[1];
       }
     } else {
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
-          uint32_t w[1];
-          load_packed<CPL, false>(P.packed + pr * P.ldp, col0, N, (P.vec & 1) != 0, w);
-          raw[st][r] = w[0];
-        }
       load_scales<CPL, false>(P.scale + (int64_t)g * P.lds, col0, N, (P.vec & 1) != 0, s);
     }
+  };
+  auto load_b = [&](int g, uint32_t (&raw)[4][4], float (&s)[CPL]) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) load_b_step(g, st, raw[st]);
+    load_scales_b(g, s);
   };
 
   W4A16_MARK(0);
@@ -721,33 +746,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
     for (int t = 0; t < CPL; ++t) U[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  uint32_t raw[4][4];
-  float s[CPL];
+  // raw: packed weights of the current group's 4 K steps; raw_n: the next
+  // group's, loaded one group ahead.
+  uint32_t raw[4][4], raw_n[4][4];
+  float s[CPL], s_n[CPL];
   float s_ref[CPL];  // scale U is currently expressed in (per column)
   load_b(g_begin, raw, s);
-  stage_a(g_begin, 0);
+  stage_a(g_begin, std::integral_constant<int, 0>{});
   W4A16_MARK(1);
 #pragma unroll
   for (int t = 0; t < CPL; ++t) s_ref[t] = clamp_scale(s[t]);
 
-  for (int g = g_begin; g < g_end; ++g) {
-    const int b = (g - g_begin) & 1;
+  // One group.  BUF is the LDS buffer holding this group's activations; the
+  // next group is staged into the other one.  BUF is a compile-time constant
+  // (the loop below is unrolled by two) so that the compiler can tell the
+  // direct-to-LDS copies into buffer BUF ^ 1 from the reads of buffer BUF:
+  // with a run-time index it must assume they alias and waits for the copies
+  // (vmcnt(0)) before the first LDS read, which serializes the prefetch.
+  auto group = [&](auto buf_tag, int g) {
+    constexpr int b = decltype(buf_tag)::value;
+    const u32x4_t* as = a_buf(buf_tag);
+    const float* cs = c_buf(buf_tag);
     // Direct-to-LDS copies of this group (issued one iteration earlier) must
     // have landed before the barrier publishes them.
     wait_vmem();
     __syncthreads();
 
     const bool has_next = g + 1 < g_end;
-    uint32_t raw_n[4][4];
-    float s_n[CPL];
     if (has_next) {
-      stage_a(g + 1, b ^ 1);
+      stage_a(g + 1, std::integral_constant<int, b ^ 1>{});
       load_b(g + 1, raw_n, s_n);
     }
 
     // Fold: U <- U * (s_ref / s) - 136 * rowsum.  (U is zero before the first
     // group, so its ratio only has to be finite.)  s_ref / s uses the hardware
     // reciprocal: relative error ~1 ulp, the order of the fold's own rounding.
+    // With 128-column tiles (CPL 2) the fold runs as one block before the
+    // group's MFMAs; with 256-column tiles it is applied to each accumulator
+    // right before its first MFMA of the group (each measured faster for its
+    // tile width on MI355X).
     float rho[CPL];
 #pragma unroll
     for (int t = 0; t < CPL; ++t) {
@@ -755,36 +792,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       rho[t] = s_ref[t] * __builtin_amdgcn_rcpf(sc);
       s_ref[t] = sc;
     }
+    constexpr bool kFoldBlock = CPL == 2;
+    if constexpr (kFoldBlock) {
 #pragma unroll
-    for (int i = 0; i < kGemmMT; ++i) {
-      const f32x4_t c4 = *reinterpret_cast<const f32x4_t*>(&Cs[b][16 * i + 4 * lk]);
+      for (int i = 0; i < kGemmMT; ++i) {
+        const f32x4_t c4 = *reinterpret_cast<const f32x4_t*>(&cs[16 * i + 4 * lk]);
 #pragma unroll
-      for (int t = 0; t < CPL; ++t)
+        for (int t = 0; t < CPL; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) U[i][t][r] = __builtin_fmaf(U[i][t][r], rho[t], -c4[r]);
+          for (int r = 0; r < 4; ++r) U[i][t][r] = __builtin_fmaf(U[i][t][r], rho[t], -c4[r]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       bf16x8_t B[CPL];
       gemm_unpack<CPL>(raw[st], B);
+      // Two halves of 4 subtiles: 4 A fragments (and at step 0 the 4 row-sum
+      // vectors) in flight while the previous half's MFMAs issue.
 #pragma unroll
-      for (int i = 0; i < kGemmMT; ++i) {
-        const bf16x8_t A = __builtin_bit_cast(bf16x8_t, As[b][(st * kGemmMT + i) * 64 + lane]);
+      for (int h = 0; h < 2; ++h) {
+        bf16x8_t A[kGemmMT / 2];
+        f32x4_t c4[kGemmMT / 2];
 #pragma unroll
-        for (int t = 0; t < CPL; ++t) U[i][t] = mfma16(A, B[t], U[i][t]);
+        for (int ii = 0; ii < kGemmMT / 2; ++ii) {
+          const int i = h * (kGemmMT / 2) + ii;
+          A[ii] = __builtin_bit_cast(bf16x8_t, as[(st * kGemmMT + i) * 64 + lane]);
+          if (!kFoldBlock && st == 0) c4[ii] = *reinterpret_cast<const f32x4_t*>(&cs[16 * i + 4 * lk]);
+        }
+#pragma unroll
+        for (int ii = 0; ii < kGemmMT / 2; ++ii) {
+          const int i = h * (kGemmMT / 2) + ii;
+#pragma unroll
+          for (int t = 0; t < CPL; ++t) {
+            if (!kFoldBlock && st == 0) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) U[i][t][r] = __builtin_fmaf(U[i][t][r], rho[t], -c4[ii][r]);
+            }
+            U[i][t] = mfma16(A[ii], B[t], U[i][t]);
+          }
+        }
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
-
     if (has_next) {
+#pragma unroll
+      for (int t = 0; t < CPL; ++t) s[t] = s_n[t];
 #pragma unroll
       for (int st = 0; st < 4; ++st)
 #pragma unroll
         for (int r = 0; r < 4; ++r) raw[st][r] = raw_n[st][r];
-#pragma unroll
-      for (int t = 0; t < CPL; ++t) s[t] = s_n[t];
     }
+  };
+  for (int g = g_begin; g < g_end; g += 2) {
+    group(std::integral_constant<int, 0>{}, g);
+    if (g + 1 < g_end) group(std::integral_constant<int, 1>{}, g + 1);
   }
 
   // ---- output: lane holds rows m0 + 16i + 4lk + r, columns col0 .. col0+CPL-1 ----
