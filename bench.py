@@ -181,7 +181,7 @@ def roofline_decode(us: float) -> dict:
         "unit": "GB/s",
         "frac": round(ach / HBM_PEAK_GBS, 4),
         "traffic": read_traffic(TRAFFIC_FILE),
-        "kernel": "gemv_kernel<8, true> (gate_proj K=4096 N=12288 M=1, one launch of int4_matmul)",
+        "kernel": "gemv_kernel<8, 4, true, false, 1> (gate_proj K=4096 N=12288 M=1, one launch of int4_matmul)",
         "bytes_per_launch": b,
         "avg_launch_us": round(us, 3),
     }
