@@ -65,9 +65,9 @@ struct Prep {
 };
 
 __device__ __forceinline__ Prep prep(uint32_t raw) {
-  const uint32_t p = raw ^ 0x88888888u;       // q + 8 in every nibble
-  const uint32_t lo = p & 0x0F0F0F0Fu;        // odd rows
-  const uint32_t hi = (p >> 4) & 0x0F0F0F0Fu;  // even rows
+  // q + 8 = q ^ 8 per nibble; xor-and with constants is one v_bitop3 each.
+  const uint32_t lo = (raw ^ 0x08080808u) & 0x0F0F0F0Fu;         // odd rows
+  const uint32_t hi = ((raw >> 4) ^ 0x08080808u) & 0x0F0F0F0Fu;  // even rows
   // v_perm_b32 byte pool: bytes 0-3 come from the second operand, 4-7 from the first.
   Prep w;
   w.x01 = __builtin_amdgcn_perm(hi, lo, 0x01050004u);

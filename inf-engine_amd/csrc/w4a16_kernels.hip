@@ -746,16 +746,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
     for (int t = 0; t < CPL; ++t) U[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // raw: packed weights of the current group's 4 K steps; raw_n: the next
-  // group's, loaded one group ahead.
-  uint32_t raw[4][4], raw_n[4][4];
-  float s[CPL], s_n[CPL];
+  // Packed weights (4 K steps) and scales of two groups: the group computed
+  // from set BUF while the next one loads into set BUF ^ 1 (the same
+  // compile-time ping-pong as the LDS buffers, so no register copies).
+  uint32_t raw2[2][4][4];
+  float s2[2][CPL];
   float s_ref[CPL];  // scale U is currently expressed in (per column)
-  load_b(g_begin, raw, s);
+  load_b(g_begin, raw2[0], s2[0]);
   stage_a(g_begin, std::integral_constant<int, 0>{});
   W4A16_MARK(1);
 #pragma unroll
-  for (int t = 0; t < CPL; ++t) s_ref[t] = clamp_scale(s[t]);
+  for (int t = 0; t < CPL; ++t) s_ref[t] = clamp_scale(s2[0][t]);
 
   // One group.  BUF is the LDS buffer holding this group's activations; the
   // next group is staged into the other one.  BUF is a compile-time constant
@@ -767,6 +768,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     constexpr int b = decltype(buf_tag)::value;
     const u32x4_t* as = a_buf(buf_tag);
     const float* cs = c_buf(buf_tag);
+    uint32_t (&raw)[4][4] = raw2[b];
+    const float (&s)[CPL] = s2[b];
     // Direct-to-LDS copies of this group (issued one iteration earlier) must
     // have landed before the barrier publishes them.
     wait_vmem();
@@ -775,7 +778,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     const bool has_next = g + 1 < g_end;
     if (has_next) {
       stage_a(g + 1, std::integral_constant<int, b ^ 1>{});
-      load_b(g + 1, raw_n, s_n);
+      load_b(g + 1, raw2[b ^ 1], s2[b ^ 1]);
     }
 
     // Fold: U <- U * (s_ref / s) - 136 * rowsum.  (U is zero before the first
@@ -833,14 +836,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
           }
         }
       }
-    }
-    if (has_next) {
-#pragma unroll
-      for (int t = 0; t < CPL; ++t) s[t] = s_n[t];
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) raw[st][r] = raw_n[st][r];
     }
   };
   for (int g = g_begin; g < g_end; g += 2) {
