@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 4
+#define W4A16_ABI_VERSION 5
 
 /* Most problems one grouped call accepts. */
 #define W4A16_MAX_PROBLEMS 16
@@ -126,6 +126,31 @@ int w4a16_linear_grouped(const w4a16_problem* problems, int count, int group_siz
 
 /* Workspace bytes w4a16_linear_grouped needs for this problem table. */
 int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int group_size, size_t* bytes);
+
+/*
+ * SwiGLU gate/up pair: h[M, N] = silu(x @ Wg) * (x @ Wu), silu(v) = v *
+ * sigmoid(v), with Wg and Wu INT4 weights of the same shape in the layout
+ * above (their own leading dimensions), bf16 h with row stride ldh.
+ *
+ * Replaces `silu(linear(x, gate)) * linear(x, up)` of the reference MLP
+ * (engine/llama_mlp.py:30-32, engine/llama_moe.py:44), i.e. two int4_matmul
+ * launches plus two elementwise kernels.  M <= 16 runs one decode launch that
+ * streams both weights and applies the epilogue to the fp32 sums (the
+ * reference rounds gate and up to bf16 first; results agree to bf16 rounding).
+ * Larger M computes gate into h and up into workspace, then one elementwise
+ * pass.  Status codes, group_size and workspace rules as w4a16_linear, with
+ * w4a16_workspace_size_swiglu() in place of w4a16_workspace_size().
+ */
+int w4a16_swiglu(const void* x, int64_t ldx,
+                 const int8_t* gate_packed, int64_t gate_ldp, const float* gate_scale, int64_t gate_lds,
+                 const int8_t* up_packed, int64_t up_ldp, const float* up_scale, int64_t up_lds,
+                 void* h, int64_t ldh,
+                 int M, int N, int K, int group_size,
+                 void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/* Workspace bytes w4a16_swiglu needs for an (M, N, K) call (0: none). */
+int w4a16_workspace_size_swiglu(int M, int N, int K, int group_size, size_t* bytes);
 
 /*
  * Dense bf16 GEMV for decode: y[m, n] = sum_k x[m, k] * w[n, k] with w in

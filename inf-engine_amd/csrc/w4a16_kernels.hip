@@ -116,50 +116,24 @@ __device__ __forceinline__ uint32_t publish_bits(float v) {
   return ~b;
 }
 
-// EPT: most elements (rows x columns of the strip) one thread handles.  The
-// finisher keeps all of a thread's polls for a chunk of splits in flight at
-// once, so a thread with several elements waits about one round trip per
-// chunk rather than one per element.
-template <int NT, int EPT, class PartialFn>
-__device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split, int n0, int wcols, int rows,
-                                              PartialFn partial) {
-  constexpr int SCH = EPT >= 8 ? 2 : (EPT >= 4 ? 4 : 8);  // splits per chunk: EPT * SCH polls in flight
-  const int N = P.N;
-  const int elems = rows * wcols;
-  const size_t stride = (size_t)M * N;
-  uint32_t* slots = reinterpret_cast<uint32_t*>(P.part);
-  const int last = P.nsplit - 1;
-  if (split != last) {
-    uint32_t* dst = slots + (size_t)split * stride;
-    for (int e = threadIdx.x; e < elems; e += NT) {
-      const int m = e / wcols, c = e % wcols, n = n0 + c;
-      if (n < N) __hip_atomic_store(dst + (size_t)m * N + n, publish_bits(partial(e)), __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-    }
-    return;
-  }
-  size_t off[EPT];
-  bool ok[EPT];
-  float own[EPT], v[EPT];
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int e = threadIdx.x + j * NT;
-    const int m = e / wcols, c = e % wcols, n = n0 + c;
-    ok[j] = e < elems && n < N;
-    off[j] = ok[j] ? (size_t)m * N + n : 0;
-    own[j] = ok[j] ? partial(e) : 0.f;
-    v[j] = 0.f;
-  }
-  bool timed_out = false;
-  for (int sp0 = 0; sp0 < last; sp0 += SCH) {
+// Poll-and-sum of nslots published slots (stride elements apart) for a
+// thread's EPT elements.  All of a thread's polls for a chunk of SCH slots are
+// in flight at once, so a thread with several elements waits about one round
+// trip per chunk rather than one per element.  Sums in slot order into v;
+// zeroes what it read.
+template <int EPT>
+__device__ __forceinline__ void sum_slots(uint32_t* slots, int nslots, size_t stride, const size_t (&off)[EPT],
+                                          const bool (&ok)[EPT], float (&v)[EPT], bool& timed_out) {
+  constexpr int SCH = EPT >= 8 ? 2 : (EPT >= 4 ? 4 : 8);  // slots per chunk: EPT * SCH polls in flight
+  for (int sp0 = 0; sp0 < nslots; sp0 += SCH) {
     uint32_t t[EPT][SCH];
 #pragma unroll
     for (int j = 0; j < EPT; ++j)
 #pragma unroll
       for (int i = 0; i < SCH; ++i)
-        t[j][i] = ok[j] && sp0 + i < last ? __hip_atomic_load(slots + (size_t)(sp0 + i) * stride + off[j],
-                                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                          : 1u;
+        t[j][i] = ok[j] && sp0 + i < nslots ? __hip_atomic_load(slots + (size_t)(sp0 + i) * stride + off[j],
+                                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                            : 1u;
     for (uint32_t spins = 0;; ++spins) {
       bool missing = false;
 #pragma unroll
@@ -183,16 +157,75 @@ __device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split
     for (int j = 0; j < EPT; ++j)
 #pragma unroll
       for (int i = 0; i < SCH; ++i)
-        if (sp0 + i < last) v[j] += __uint_as_float(~t[j][i]);
+        if (sp0 + i < nslots) v[j] += __uint_as_float(~t[j][i]);
+  }
+#pragma unroll
+  for (int j = 0; j < EPT; ++j)
+    if (ok[j])
+      for (int sp = 0; sp < nslots; ++sp)
+        __hip_atomic_store(slots + (size_t)sp * stride + off[j], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// x * sigmoid(x) in fp32 (engine/layers.py:28-30).
+__device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); }
+
+// Split-K epilogue modes.
+enum FinishMode {
+  kFinishStore = 0,  // last split sums the partials and stores bf16 y
+  kFinishGate = 1,   // gate of a SwiGLU pair: every split publishes (slots [nsplit][M][N])
+  kFinishUp = 2,     // up of a SwiGLU pair: the last split also sums the gate's slots
+                     // (problem `gate`) and stores bf16(silu(gate) * up)
+};
+
+// EPT: most elements (rows x columns of the strip) one thread handles.
+template <int NT, int EPT, int MODE, class PartialFn>
+__device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split, int n0, int wcols, int rows,
+                                              PartialFn partial, const Problem* gate = nullptr) {
+  const int N = P.N;
+  const int elems = rows * wcols;
+  const size_t stride = (size_t)M * N;
+  uint32_t* slots = reinterpret_cast<uint32_t*>(P.part);
+  const int last = P.nsplit - 1;
+  if (MODE == kFinishGate || split != last) {
+    uint32_t* dst = slots + (size_t)split * stride;
+    for (int e = threadIdx.x; e < elems; e += NT) {
+      const int m = e / wcols, c = e % wcols, n = n0 + c;
+      if (n < N) __hip_atomic_store(dst + (size_t)m * N + n, publish_bits(partial(e)), __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  size_t off[EPT];
+  bool ok[EPT];
+  float own[EPT], v[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = threadIdx.x + j * NT;
+    const int m = e / wcols, c = e % wcols, n = n0 + c;
+    ok[j] = e < elems && n < N;
+    off[j] = ok[j] ? (size_t)m * N + n : 0;
+    own[j] = ok[j] ? partial(e) : 0.f;
+    v[j] = 0.f;
+  }
+  bool timed_out = false;
+  sum_slots<EPT>(slots, last, stride, off, ok, v, timed_out);
+  if constexpr (MODE == kFinishUp) {
+    float gv[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) gv[j] = 0.f;
+    sum_slots<EPT>(reinterpret_cast<uint32_t*>(gate->part), gate->nsplit, stride, off, ok, gv, timed_out);
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) v[j] = silu(gv[j]) * (v[j] + own[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) v[j] += own[j];
   }
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
     if (!ok[j]) continue;
     const int e = threadIdx.x + j * NT;
     const int m = e / wcols, n = n0 + e % wcols;
-    P.y[(int64_t)m * P.ldy + n] = timed_out ? (uint16_t)0x7fc0 : f32_to_bf16(v[j] + own[j]);
-    for (int sp = 0; sp < last; ++sp)
-      __hip_atomic_store(slots + (size_t)sp * stride + off[j], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    P.y[(int64_t)m * P.ldy + n] = timed_out ? (uint16_t)0x7fc0 : f32_to_bf16(v[j]);
   }
 }
 
@@ -260,14 +293,77 @@ __device__ __forceinline__ void decode_group(const DecodeSlot<CPL>& d, const bf1
     for (int r = 0; r < 4; ++r) total[t][r] = __builtin_fmaf(acc[t][r], d.s[t], total[t][r]);
 }
 
+// One wave's share of a decode launch: the 128-row group g of problem P for
+// the lane's CPL columns starting at col0, accumulated into total.  Activation
+// fragments: lane (lc, lk) holds x[lc, g*128 + 32*st + 8*lk .. +8].  FULL
+// launches load them unconditionally (lanes past M read row 0) and zero them
+// with a select, so no branch or wait sits before the weight loads.
+template <int CPL, bool FULL>
+__device__ __forceinline__ void decode_wave(const Problem& P, int g, int col0, int lc, int lk, int M,
+                                            f32x4_t (&total)[CPL]) {
+  const int N = P.N;
+  const int G = (uint32_t)P.K / kGroup;
+  bf16x8_t A[4];
+  const uint32_t keep = lc < M ? 0xffffffffu : 0u;
+  DecodeSlot<CPL> d;
+  if constexpr (FULL) {
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(P.x, (uint32_t)((size_t)P.ldx * 2 * M));
+    const uint32_t xoff = ((uint32_t)(lc < M ? lc : 0) * (uint32_t)P.ldx + (uint32_t)(g * kGroup + lk * 8)) * 2u;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + st * 64, 0, 0));
+      A[st] = as_bf16x8(v & keep);
+    }
+  } else {
+    const bool vec_x = (P.vec & 2) != 0;
+    const uint16_t* xrow = P.x + (int64_t)(lc < M ? lc : 0) * P.ldx + (int64_t)g * kGroup + lk * 8;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) A[st] = as_bf16x8(__builtin_bit_cast(u32x4_t, load_x8(xrow + st * 32, vec_x)) & keep);
+  }
+  if constexpr (FULL) {
+    const uint32_t ldp = (uint32_t)P.ldp;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(P.packed, (uint32_t)((size_t)(P.K / 2) * P.ldp));
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(P.scale, (uint32_t)((size_t)G * P.lds * 4));
+    const uint32_t soff = (uint32_t)g * (uint32_t)P.lds * 4u;
+#pragma unroll
+    for (int t = 0; t < CPL; t += 4) {
+      const f32x4_t v = __builtin_bit_cast(
+          f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, (uint32_t)(col0 + t) * 4u, soff, 0));
+      d.s[t] = v[0]; d.s[t + 1] = v[1]; d.s[t + 2] = v[2]; d.s[t + 3] = v[3];
+    }
+    const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
+    const uint32_t gbase = (uint32_t)g * kPackedRowsPerGroup * ldp;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        buffer_load_bytes<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, d.raw[st][r]);
+  } else {
+    const bool vw = (P.vec & 1) != 0;
+    load_scales<CPL, false>(P.scale + (int64_t)g * P.lds, col0, N, vw, d.s);
+    const uint8_t* base = P.packed + (int64_t)g * kPackedRowsPerGroup * P.ldp;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        load_packed<CPL, false>(base + (int64_t)(st * 16 + lk * 4 + r) * P.ldp, col0, N, vw, d.raw[st][r]);
+  }
+  // Everything above is in flight before the first MFMA below.
+  __builtin_amdgcn_sched_barrier(0);
+  W4A16_MARK(1);
+  decode_group<CPL>(d, A, total);
+}
+
 // MULTI: the launch holds several problems.  A single-problem launch reads its
 // table entry at fixed kernel-argument offsets, so every field arrives with one
 // round of scalar loads instead of two dependent ones.  MROWS (1, 4, 8 or 16)
 // bounds M for every problem of the launch.  MROWS == 1 (batch-1 decode)
 // compiles the row loops and reductions to their one-row form, which measures
 // ~0.4 us faster per launch; the bound also sizes the split-K finisher's
-// per-thread polls (splitk_finish).
-template <int CPL, int WAVES, bool FULL, bool MULTI, int MROWS>
+// per-thread polls (splitk_finish).  PAIR: the launch is a SwiGLU pair, gate
+// (problem 0) and up (problem 1) of the same shape and activations; gate's
+// workgroups publish every split and up's finisher stores silu(gate) * up.
+template <int CPL, int WAVES, bool FULL, bool MULTI, int MROWS, bool PAIR = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
   constexpr int WCOLS = 16 * CPL;
   constexpr int NT = WAVES * 64;
@@ -305,60 +401,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
   f32x4_t total[CPL];
 #pragma unroll
   for (int t = 0; t < CPL; ++t) total[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  if (active) {
-    // Activation fragments: lane (lc, lk) holds x[lc, g*128 + 32*st + 8*lk .. +8].
-    // FULL launches load them unconditionally (lanes past M read row 0) and
-    // zero them with a select, so no branch or wait sits before the weight loads.
-    bf16x8_t A[4];
-    const uint32_t keep = lc < M ? 0xffffffffu : 0u;
-    DecodeSlot<CPL> d;
-    if constexpr (FULL) {
-      const __amdgpu_buffer_rsrc_t xrs = make_rsrc(P.x, (uint32_t)((size_t)P.ldx * 2 * M));
-      const uint32_t xoff = ((uint32_t)(lc < M ? lc : 0) * (uint32_t)P.ldx + (uint32_t)(g * kGroup + lk * 8)) * 2u;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + st * 64, 0, 0));
-        A[st] = as_bf16x8(v & keep);
-      }
-    } else {
-      const bool vec_x = (P.vec & 2) != 0;
-      const uint16_t* xrow = P.x + (int64_t)(lc < M ? lc : 0) * P.ldx + (int64_t)g * kGroup + lk * 8;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) A[st] = as_bf16x8(__builtin_bit_cast(u32x4_t, load_x8(xrow + st * 32, vec_x)) & keep);
-    }
-    if constexpr (FULL) {
-      const uint32_t ldp = (uint32_t)P.ldp;
-      const __amdgpu_buffer_rsrc_t wrs = make_rsrc(P.packed, (uint32_t)((size_t)(P.K / 2) * P.ldp));
-      const __amdgpu_buffer_rsrc_t srs = make_rsrc(P.scale, (uint32_t)((size_t)G * P.lds * 4));
-      const uint32_t soff = (uint32_t)g * (uint32_t)P.lds * 4u;
-#pragma unroll
-      for (int t = 0; t < CPL; t += 4) {
-        const f32x4_t v = __builtin_bit_cast(
-            f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, (uint32_t)(col0 + t) * 4u, soff, 0));
-        d.s[t] = v[0]; d.s[t + 1] = v[1]; d.s[t + 2] = v[2]; d.s[t + 3] = v[3];
-      }
-      const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
-      const uint32_t gbase = (uint32_t)g * kPackedRowsPerGroup * ldp;
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          buffer_load_bytes<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, d.raw[st][r]);
-    } else {
-      const bool vw = (P.vec & 1) != 0;
-      load_scales<CPL, false>(P.scale + (int64_t)g * P.lds, col0, N, vw, d.s);
-      const uint8_t* base = P.packed + (int64_t)g * kPackedRowsPerGroup * P.ldp;
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          load_packed<CPL, false>(base + (int64_t)(st * 16 + lk * 4 + r) * P.ldp, col0, N, vw, d.raw[st][r]);
-    }
-    // Everything above is in flight before the first MFMA below.
-    __builtin_amdgcn_sched_barrier(0);
-    W4A16_MARK(1);
-    decode_group<CPL>(d, A, total);
-  }
+  if (active) decode_wave<CPL, FULL>(P, g, col0, lc, lk, M, total);
   W4A16_MARK(3);
 
   // Reduce the waves through LDS.  Rows m = 4*lk + r of the MFMA output.
@@ -382,6 +425,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
     for (int w = 1; w < WAVES; ++w) v += red[(size_t)w * elems + e];
     return v;
   };
+  constexpr int EPT = (MROWS * WCOLS + NT - 1) / NT;
+  if constexpr (PAIR) {
+    if (pi == 0)
+      splitk_finish<NT, EPT, kFinishGate>(P, M, split, n0, WCOLS, M, wave_sum);
+    else
+      splitk_finish<NT, EPT, kFinishUp>(P, M, split, n0, WCOLS, M, wave_sum, &L.p[0]);
+    return;
+  }
   if (P.nsplit == 1) {
     for (int e = threadIdx.x; e < elems; e += NT) {
       const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
@@ -390,7 +441,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
     W4A16_MARK(5);
     return;
   }
-  splitk_finish<NT, (MROWS * WCOLS + NT - 1) / NT>(P, M, split, n0, WCOLS, M, wave_sum);
+  splitk_finish<NT, EPT, kFinishStore>(P, M, split, n0, WCOLS, M, wave_sum);
   W4A16_MARK(6);
 }
 
@@ -525,7 +576,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(Launch L) {
     }
     return;
   }
-  splitk_finish<256, 32 * WCOLS / 256>(P, M, split, n0, WCOLS, M, wave_sum);
+  splitk_finish<256, 32 * WCOLS / 256, kFinishStore>(P, M, split, n0, WCOLS, M, wave_sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -1079,6 +1130,17 @@ __global__ __launch_bounds__(256) void zero_kernel(uint16_t* __restrict__ y, int
   y[(idx / N) * ldy + idx % N] = 0;
 }
 
+// h = bf16(silu(h) * u) elementwise: the SwiGLU epilogue after separate gate
+// (written to h) and up (u, contiguous [M, N]) projections.
+__global__ __launch_bounds__(256) void silu_mul_kernel(uint16_t* __restrict__ h, int64_t ldh,
+                                                       const uint16_t* __restrict__ u, int M, int N) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  const int64_t m = i / N, n = i % N;
+  uint16_t* d = h + m * ldh + n;
+  *d = f32_to_bf16(silu(bf16_to_f32(*d)) * bf16_to_f32(u[i]));
+}
+
 // ---------------------------------------------------------------------------
 // Host-side planning.
 // ---------------------------------------------------------------------------
@@ -1102,6 +1164,8 @@ struct Plan {
   int cpl;
   int waves;           // gemv: waves per workgroup (4 or 8)
   bool full;           // every problem takes the unconditional (aligned, full tile) load path
+  bool pair;           // SwiGLU pair (gemv only): problem 0 gate, problem 1 up
+  size_t skip;         // bytes at the start of the upper workspace half reserved by the caller
   size_t lds_bytes;    // dynamic LDS (gemv / skinny)
   size_t ws_bytes;     // bytes of the plan's workspace half (see bind())
   int total_wgs;
@@ -1129,8 +1193,9 @@ inline Kind kind_of(int M) { return M <= 16 ? kGemv : (M <= 32 ? kSkinny : kGemm
 
 // Plan one launch over problems that all have M > 0, N > 0, K > 0 and the
 // same kind (kind_of(M)); the skinny kernel takes a single problem.
-Plan make_plan(const w4a16_problem* probs, int count) {
+Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
   Plan pl{};
+  pl.pair = pair;
   pl.L.count = count;
   int max_m = 0;
   for (int i = 0; i < count; ++i) max_m = std::max(max_m, probs[i].M);
@@ -1213,9 +1278,12 @@ Plan make_plan(const w4a16_problem* probs, int count) {
       const size_t xbytes = (size_t)P.ldx * 2 * M;
       full = full && (P.vec & 1) && P.N % wcols == 0 && wbytes < 0xffffffffull && sbytes < 0xffffffffull;
       if (pl.kind == kGemv) full = full && (P.vec & 2) && xbytes < 0xffffffffull;
-      if (P.nsplit > 1) {
+      // Published slots: nsplit - 1 per strip (the last split finishes), all
+      // nsplit for the gate of a pair (up's finisher reads them).
+      const int nslots = pair && i == 0 ? P.nsplit : P.nsplit - 1;
+      if (nslots > 0) {
         pl.part_off[i] = ws;
-        ws = align256(ws + (size_t)(P.nsplit - 1) * M * P.N * 4);
+        ws = align256(ws + (size_t)nslots * M * P.N * 4);
       }
     }
     pl.lds_bytes = lds;
@@ -1286,13 +1354,13 @@ Plan make_plan(const w4a16_problem* probs, int count) {
 // slots rely on "0 = empty" whatever ran before on the same workspace.
 void bind(Plan& pl, void* workspace, size_t workspace_bytes) {
   char* ws = static_cast<char*>(workspace);
-  char* upper = ws + ((workspace_bytes / 2) & ~(size_t)255);
+  char* upper = ws + ((workspace_bytes / 2) & ~(size_t)255) + pl.skip;
   for (int i = 0; i < pl.L.count; ++i) {
     Problem& P = pl.L.p[i];
     if (pl.kind == kGemm) {
       if (P.nsplit > 1) P.part = reinterpret_cast<float*>(upper + pl.part_off[i]);
       P.rowsum = reinterpret_cast<float*>(upper + pl.rowsum_off[pl.rowsum_src[i]]);
-    } else if (P.nsplit > 1) {
+    } else if (P.nsplit > 1 || (pl.pair && i == 0)) {
       P.part = reinterpret_cast<float*>(ws + pl.part_off[i]);
     }
   }
@@ -1302,40 +1370,47 @@ void bind(Plan& pl, void* workspace, size_t workspace_bytes) {
 #endif
 }
 
-// Workspace bytes a plan needs: twice its half, rounded.
-size_t plan_bytes(const Plan& pl) { return pl.ws_bytes == 0 ? 0 : 2 * align256(pl.ws_bytes) + 256; }
+// Workspace bytes a plan needs: twice its half, rounded.  The GEMM scratch
+// sits after the caller's `skip` bytes in the upper half; decode slots use the
+// lower half, which must then still be as large as `skip`.
+size_t plan_bytes(const Plan& pl) {
+  const size_t half = pl.kind == kGemm ? pl.skip + pl.ws_bytes : std::max(pl.skip, pl.ws_bytes);
+  return half == 0 ? 0 : 2 * align256(half) + 256;
+}
 
 int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? W4A16_OK : W4A16_ERR_LAUNCH;
 }
 
-template <int CPL, int WAVES, bool MULTI, int MROWS>
+template <int CPL, int WAVES, bool MULTI, int MROWS, bool PAIR>
 void launch_gemv_as(const Plan& pl, dim3 grid, hipStream_t s) {
   const dim3 block(WAVES * 64);
   if (pl.full)
-    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, true, MULTI, MROWS>), grid, block, pl.lds_bytes, s, pl.L);
+    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, true, MULTI, MROWS, PAIR>), grid, block, pl.lds_bytes, s, pl.L);
   else
-    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, false, MULTI, 16>), grid, block, pl.lds_bytes, s, pl.L);
+    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, false, MULTI, 16, PAIR>), grid, block, pl.lds_bytes, s, pl.L);
 }
 
-template <int CPL, int WAVES, bool MULTI>
+template <int CPL, int WAVES, bool MULTI, bool PAIR = false>
 void launch_gemv_rows(const Plan& pl, dim3 grid, int max_m, hipStream_t s) {
   if (max_m == 1)
-    launch_gemv_as<CPL, WAVES, MULTI, 1>(pl, grid, s);
+    launch_gemv_as<CPL, WAVES, MULTI, 1, PAIR>(pl, grid, s);
   else if (max_m <= 4)
-    launch_gemv_as<CPL, WAVES, MULTI, 4>(pl, grid, s);
+    launch_gemv_as<CPL, WAVES, MULTI, 4, PAIR>(pl, grid, s);
   else if (max_m <= 8)
-    launch_gemv_as<CPL, WAVES, MULTI, 8>(pl, grid, s);
+    launch_gemv_as<CPL, WAVES, MULTI, 8, PAIR>(pl, grid, s);
   else
-    launch_gemv_as<CPL, WAVES, MULTI, 16>(pl, grid, s);
+    launch_gemv_as<CPL, WAVES, MULTI, 16, PAIR>(pl, grid, s);
 }
 
 template <int CPL, int WAVES>
 int launch_gemv(const Plan& pl, hipStream_t s) {
   int max_m = 0;
   for (int i = 0; i < pl.L.count; ++i) max_m = std::max(max_m, pl.L.p[i].M);
-  if (pl.L.count > 1)
+  if (pl.pair)
+    launch_gemv_rows<CPL, WAVES, true, true>(pl, dim3(pl.total_wgs), max_m, s);
+  else if (pl.L.count > 1)
     launch_gemv_rows<CPL, WAVES, true>(pl, dim3(pl.total_wgs), max_m, s);
   else
     launch_gemv_rows<CPL, WAVES, false>(pl, dim3(pl.L.p[0].tiles_n, pl.L.p[0].nsplit), max_m, s);
@@ -1397,8 +1472,10 @@ int for_each_chunk(const w4a16_problem& q, Fn fn) {
 }
 
 // Launch one planned batch (all problems of one kind).
-int launch_plan(const w4a16_problem* probs, int count, void* workspace, size_t workspace_bytes, hipStream_t s) {
-  Plan pl = make_plan(probs, count);
+int launch_plan(const w4a16_problem* probs, int count, void* workspace, size_t workspace_bytes, hipStream_t s,
+                size_t skip = 0, bool pair = false) {
+  Plan pl = make_plan(probs, count, pair);
+  pl.skip = skip;
   const size_t need = plan_bytes(pl);
   if (need > 0 && (!workspace || workspace_bytes < need)) return W4A16_ERR_WORKSPACE;
   bind(pl, workspace, workspace_bytes);
@@ -1423,14 +1500,16 @@ int launch_plan(const w4a16_problem* probs, int count, void* workspace, size_t w
 }
 
 // Workspace bytes launch_plan needs for one batch.
-int plan_workspace(const w4a16_problem* probs, int count, size_t* bytes) {
-  const Plan pl = make_plan(probs, count);
+int plan_workspace(const w4a16_problem* probs, int count, size_t* bytes, size_t skip = 0, bool pair = false) {
+  Plan pl = make_plan(probs, count, pair);
+  pl.skip = skip;
   *bytes = std::max(*bytes, plan_bytes(pl));
   return W4A16_OK;
 }
 
 // The launches run in order on one stream, so they share the workspace.
-int run(const w4a16_problem* probs, int count, void* workspace, size_t workspace_bytes, hipStream_t s) {
+int run(const w4a16_problem* probs, int count, void* workspace, size_t workspace_bytes, hipStream_t s,
+        size_t skip = 0) {
   Batches b = split(probs, count);
   for (int i = 0; i < b.n_sep; ++i) {
     const w4a16_problem& q = b.sep[i];
@@ -1440,37 +1519,79 @@ int run(const w4a16_problem* probs, int count, void* workspace, size_t workspace
                          static_cast<uint16_t*>(q.y), q.ldy, q.M, q.N);
       rc = launch_status();
     } else {
-      rc = for_each_chunk(q, [&](const w4a16_problem& c) { return launch_plan(&c, 1, workspace, workspace_bytes, s); });
+      rc = for_each_chunk(q, [&](const w4a16_problem& c) {
+        return launch_plan(&c, 1, workspace, workspace_bytes, s, skip);
+      });
     }
     if (rc != W4A16_OK) return rc;
   }
   if (b.n_gemv > 0) {
-    const int rc = launch_plan(b.gemv, b.n_gemv, workspace, workspace_bytes, s);
+    const int rc = launch_plan(b.gemv, b.n_gemv, workspace, workspace_bytes, s, skip);
     if (rc != W4A16_OK) return rc;
   }
   for (int i = 0; i < b.n_skinny; ++i) {
-    const int rc = launch_plan(&b.skinny[i], 1, workspace, workspace_bytes, s);
+    const int rc = launch_plan(&b.skinny[i], 1, workspace, workspace_bytes, s, skip);
     if (rc != W4A16_OK) return rc;
   }
-  if (b.n_gemm > 0) return launch_plan(b.gemm, b.n_gemm, workspace, workspace_bytes, s);
+  if (b.n_gemm > 0) return launch_plan(b.gemm, b.n_gemm, workspace, workspace_bytes, s, skip);
   return W4A16_OK;
 }
 
 // Workspace run() needs for these problems (0 when none).
-int workspace_for(const w4a16_problem* probs, int count, size_t* bytes) {
+int workspace_for(const w4a16_problem* probs, int count, size_t* bytes, size_t skip = 0) {
   *bytes = 0;
   Batches b = split(probs, count);
   for (int i = 0; i < b.n_sep; ++i) {
     if (b.sep[i].K == 0) continue;
-    const int rc = for_each_chunk(b.sep[i], [&](const w4a16_problem& c) { return plan_workspace(&c, 1, bytes); });
+    const int rc =
+        for_each_chunk(b.sep[i], [&](const w4a16_problem& c) { return plan_workspace(&c, 1, bytes, skip); });
     if (rc != W4A16_OK) return rc;
   }
   int rc = W4A16_OK;
-  if (b.n_gemv > 0 && (rc = plan_workspace(b.gemv, b.n_gemv, bytes)) != W4A16_OK) return rc;
+  if (b.n_gemv > 0 && (rc = plan_workspace(b.gemv, b.n_gemv, bytes, skip)) != W4A16_OK) return rc;
   for (int i = 0; i < b.n_skinny; ++i)
-    if ((rc = plan_workspace(&b.skinny[i], 1, bytes)) != W4A16_OK) return rc;
-  if (b.n_gemm > 0 && (rc = plan_workspace(b.gemm, b.n_gemm, bytes)) != W4A16_OK) return rc;
+    if ((rc = plan_workspace(&b.skinny[i], 1, bytes, skip)) != W4A16_OK) return rc;
+  if (b.n_gemm > 0 && (rc = plan_workspace(b.gemm, b.n_gemm, bytes, skip)) != W4A16_OK) return rc;
   return W4A16_OK;
+}
+
+// SwiGLU h = silu(x @ Wg) * (x @ Wu) on the gate/up problem pair.  M <= 16:
+// one decode launch whose finishers apply the epilogue to the fp32 sums.
+// Larger M: gate into h and up into the first `ubytes` of the upper workspace
+// half (one grouped launch), then silu_mul_kernel.
+size_t swiglu_up_bytes(int M, int N) { return M <= 16 ? 0 : align256((size_t)M * N * 2); }
+
+int swiglu(const w4a16_problem pair[2], void* workspace, size_t workspace_bytes, hipStream_t s) {
+  const w4a16_problem& g = pair[0];
+  if (g.M == 0 || g.N == 0) return W4A16_OK;
+  if (g.K == 0) {
+    hipLaunchKernelGGL(zero_kernel, dim3(ceil_div((int64_t)g.M * g.N, 256)), dim3(256), 0, s,
+                       static_cast<uint16_t*>(g.y), g.ldy, g.M, g.N);
+    return launch_status();
+  }
+  if (g.M <= 16) return launch_plan(pair, 2, workspace, workspace_bytes, s, 0, true);
+  const size_t ub = swiglu_up_bytes(g.M, g.N);
+  if (!workspace || workspace_bytes < 2 * ub + 256) return W4A16_ERR_WORKSPACE;
+  w4a16_problem q[2] = {pair[0], pair[1]};
+  uint16_t* u = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + ((workspace_bytes / 2) & ~(size_t)255));
+  q[1].y = u;
+  q[1].ldy = g.N;
+  const int rc = run(q, 2, workspace, workspace_bytes, s, ub);
+  if (rc != W4A16_OK) return rc;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(ceil_div((int64_t)g.M * g.N, 256)), dim3(256), 0, s,
+                     static_cast<uint16_t*>(g.y), g.ldy, static_cast<const uint16_t*>(u), g.M, g.N);
+  return launch_status();
+}
+
+int swiglu_workspace(const w4a16_problem pair[2], size_t* bytes) {
+  *bytes = 0;
+  const w4a16_problem& g = pair[0];
+  if (g.M == 0 || g.N == 0 || g.K == 0) return W4A16_OK;
+  if (g.M <= 16) return plan_workspace(pair, 2, bytes, 0, true);
+  const size_t ub = swiglu_up_bytes(g.M, g.N);
+  const int rc = workspace_for(pair, 2, bytes, ub);
+  *bytes = std::max(*bytes, 2 * ub + 256);
+  return rc;
 }
 
 int check_all(const w4a16_problem* probs, int count, int group_size) {
@@ -1543,6 +1664,31 @@ int w4a16_linear(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, 
   if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
   const w4a16_problem q{x, ldx, packed, ldp, scale, lds, y, ldy, M, N, K};
   return w4a16_linear_grouped(&q, 1, group_size, workspace, workspace_bytes, stream);
+}
+
+int w4a16_workspace_size_swiglu(int M, int N, int K, int group_size, size_t* bytes) {
+  if (!bytes) return W4A16_ERR_NULL;
+  *bytes = 0;
+  if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
+  if (group_size != kGroup) return W4A16_ERR_GROUP_SIZE;
+  if (K % kGroup != 0) return W4A16_ERR_K_GROUP;
+  const uintptr_t a = 256;
+  const w4a16_problem q{reinterpret_cast<const void*>(a), K, reinterpret_cast<const int8_t*>(a), N,
+                        reinterpret_cast<const float*>(a), N, reinterpret_cast<void*>(a), N, M, N, K};
+  const w4a16_problem pair[2] = {q, q};
+  return swiglu_workspace(pair, bytes);
+}
+
+int w4a16_swiglu(const void* x, int64_t ldx, const int8_t* gate_packed, int64_t gate_ldp, const float* gate_scale,
+                 int64_t gate_lds, const int8_t* up_packed, int64_t up_ldp, const float* up_scale, int64_t up_lds,
+                 void* h, int64_t ldh, int M, int N, int K, int group_size, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
+  const w4a16_problem pair[2] = {{x, ldx, gate_packed, gate_ldp, gate_scale, gate_lds, h, ldh, M, N, K},
+                                 {x, ldx, up_packed, up_ldp, up_scale, up_lds, h, ldh, M, N, K}};
+  const int rc = check_all(pair, 2, group_size);
+  if (rc != W4A16_OK) return rc;
+  return swiglu(pair, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int w4a16_bf16_gemv(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy, int M, int N,

@@ -10,13 +10,21 @@ in hand-written gfx950 HIP kernels behind the C ABI of include/w4a16.h.
 
 from .checkpoint import load_int4, load_quantized_llama, save_int4
 from . import moe
-from .layers import linear, lm_head
-from .quant import dequantize_weight_int4, int4_matmul, int4_matmul_grouped, quantize_weight_int4
+from .layers import linear, lm_head, swiglu_mlp
+from .quant import (
+    dequantize_weight_int4,
+    int4_matmul,
+    int4_matmul_grouped,
+    int4_swiglu,
+    quantize_weight_int4,
+)
 from .quantize import QuantizedLlamaWeights, _Int4Weight, quantize_llama, quantized_to_device
 
 __all__ = [
     "linear",
     "lm_head",
+    "swiglu_mlp",
+    "int4_swiglu",
     "int4_matmul",
     "int4_matmul_grouped",
     "quantize_weight_int4",

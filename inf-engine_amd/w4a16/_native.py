@@ -41,6 +41,8 @@ EXPORTED_SYMBOLS = (
     "w4a16_workspace_size_grouped",
     "w4a16_dequant",
     "w4a16_bf16_gemv",
+    "w4a16_swiglu",
+    "w4a16_workspace_size_swiglu",
 )
 
 
@@ -88,6 +90,11 @@ def load_library() -> ctypes.CDLL:
         lib.w4a16_linear.restype = i32
         lib.w4a16_dequant.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
         lib.w4a16_dequant.restype = i32
+        lib.w4a16_swiglu.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64,
+                                     i32, i32, i32, i32, vp, sz, vp]
+        lib.w4a16_swiglu.restype = i32
+        lib.w4a16_workspace_size_swiglu.argtypes = [i32, i32, i32, i32, ctypes.POINTER(sz)]
+        lib.w4a16_workspace_size_swiglu.restype = i32
         lib.w4a16_bf16_gemv.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, vp]
         lib.w4a16_bf16_gemv.restype = i32
         pp = ctypes.POINTER(Problem)
@@ -210,6 +217,35 @@ def linear_grouped(xs, weights, group_size: int) -> list[torch.Tensor]:
                                   stream)
     check(rc, "w4a16_linear_grouped")
     return outs
+
+
+def swiglu(a: torch.Tensor, gate, up, group_size: int) -> torch.Tensor:
+    """h = silu(a @ Wg) * (a @ Wu) on the current HIP stream; gate/up are (packed, fp32 scale)."""
+    lib = load_library()
+    m, k = a.shape
+    if a.stride(1) != 1:
+        a = a.contiguous()
+    ops = []
+    for packed, scale in (gate, up):
+        ops += [packed if packed.stride(1) == 1 else packed.contiguous(),
+                scale if scale.stride(1) == 1 else scale.contiguous()]
+    n = ops[0].shape[1]
+    h = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream(a.device).cuda_stream
+    nbytes = ctypes.c_size_t(0)
+    check(lib.w4a16_workspace_size_swiglu(m, n, k, group_size, ctypes.byref(nbytes)), "w4a16_workspace_size_swiglu")
+    ws = get_workspace(a.device, stream, nbytes.value)
+    rc = lib.w4a16_swiglu(
+        a.data_ptr(), a.stride(0),
+        ops[0].data_ptr(), ops[0].stride(0), ops[1].data_ptr(), ops[1].stride(0),
+        ops[2].data_ptr(), ops[2].stride(0), ops[3].data_ptr(), ops[3].stride(0),
+        h.data_ptr(), h.stride(0),
+        m, n, k, group_size,
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+        stream,
+    )
+    check(rc, "w4a16_swiglu")
+    return h
 
 
 def bf16_gemv(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:

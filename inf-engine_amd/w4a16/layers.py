@@ -17,6 +17,32 @@ def linear(x: torch.Tensor, weight) -> torch.Tensor:
     return x @ weight.T
 
 
+def silu(x: torch.Tensor) -> torch.Tensor:
+    """x * sigmoid(x) (engine/layers.py:28-30)."""
+    return x * torch.sigmoid(x)
+
+
+def swiglu_mlp(x: torch.Tensor, weights: dict) -> torch.Tensor:
+    """``down(silu(gate(x)) * up(x))`` -- the SwiGLU block of engine/llama_mlp.py:19-33.
+
+    When gate and up are INT4 weights (group size 128) on a HIP device, the
+    pair runs as one fused ``int4_swiglu`` call; anything else follows the
+    reference's three ``linear`` calls.
+    """
+    from .quant import int4_swiglu
+
+    g, u, d = weights["mlp.gate_proj.weight"], weights["mlp.up_proj.weight"], weights["mlp.down_proj.weight"]
+    fused = (
+        all(hasattr(w, "packed") and getattr(w, "group_size", None) == 128 for w in (g, u))
+        and x.is_cuda and g.shape == u.shape
+    )
+    if not fused:
+        return linear(silu(linear(x, g)) * linear(x, u), d)
+    lead = x.shape[:-1]
+    h = int4_swiglu(x.reshape(-1, x.shape[-1]), (g.packed, g.scale), (u.packed, u.scale), g.group_size)
+    return linear(h.reshape(*lead, g.shape[0]), d)
+
+
 def lm_head(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """Logits ``x @ weight.T`` for a dense bf16 ``weight[vocab, d_model]`` (engine/llama_model.py:148).
 

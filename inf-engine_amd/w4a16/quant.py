@@ -161,3 +161,22 @@ def int4_matmul(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, grou
     scale = _check_operands(a, packed, scale, group_size)
     with torch.cuda.device(a.device):
         return _native.linear(a, packed, scale, group_size)
+
+
+def int4_swiglu(a: torch.Tensor, gate, up, group_size: int = 128) -> torch.Tensor:
+    """SwiGLU gate/up pair ``silu(a @ Wg) * (a @ Wu)`` in one call.
+
+    ``gate`` and ``up`` are ``(packed, scale)`` pairs of the same shape.  The
+    reference computes ``silu(linear(x, gate)) * linear(x, up)``
+    (engine/llama_mlp.py:30-32, engine/llama_moe.py:44) as two int4_matmul
+    launches and two elementwise kernels; here M <= 16 is a single decode
+    launch with the epilogue on the fp32 sums, larger M the grouped GEMM plus
+    one elementwise pass.  Same checks and exceptions as ``int4_matmul``.
+    """
+    (gp, gs), (up_p, us) = gate, up
+    if gp.shape != up_p.shape or gs.shape != us.shape:
+        raise ValueError(f"gate {tuple(gp.shape)} and up {tuple(up_p.shape)} weights differ in shape")
+    gs = _check_operands(a, gp, gs, group_size)
+    us = _check_operands(a, up_p, us, group_size)
+    with torch.cuda.device(a.device):
+        return _native.swiglu(a, (gp, gs), (up_p, us), group_size)

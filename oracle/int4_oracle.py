@@ -14,6 +14,9 @@ Contents, each restating the reference's algorithm:
                          (engine/kernels/quant.py:186-238) in float64
 * ``cpu_path``        -- the reference's CPU branch of int4_matmul
                          (engine/kernels/quant.py:264-266) in torch on the host
+* ``silu`` / ``swiglu_reference`` -- silu (engine/layers.py:28-30) and the
+                         gate/up half of the SwiGLU MLP, silu(x @ Wg) * (x @ Wu)
+                         (engine/llama_mlp.py:30-32), in float64
 
 Byte and integer work is numpy; the CPU path is torch on the host because that
 is what the reference runs there.
@@ -30,6 +33,10 @@ How each function is pinned (tests/test_oracle.py):
                    bit-visible), and the golden fixture.
   fused_reference  brute-force triple loop on small integer problems (exact),
                    and the closed form for one-hot activations.
+  silu             closed forms: silu(0) = 0, silu(x) - silu(-x) = x,
+                   silu(x) -> x (x -> +inf) and -> 0 (x -> -inf), silu(ln 3)
+                   = 0.75 ln 3; swiglu_reference against fused_reference
+                   with an all-ones-sum up weight (u = sum of x).
   cpu_path         test_int4_quant.py:67-82 bound (rel. error < 0.25 vs the
                    unquantized product) and agreement with fused_reference
                    within bf16 rounding.
@@ -122,6 +129,24 @@ def fused_reference(x: np.ndarray, packed: np.ndarray, scale: np.ndarray, group_
     """
     w = dequantize(packed, np.asarray(scale, dtype=np.float64), group_size)
     return np.asarray(x, dtype=np.float64) @ w
+
+
+def silu(v: np.ndarray) -> np.ndarray:
+    """v * sigmoid(v) in float64 (engine/layers.py:28-30), overflow-free for large |v|."""
+    v = np.asarray(v, dtype=np.float64)
+    e = np.exp(-np.abs(v))
+    sig = np.where(v >= 0, 1.0 / (1.0 + e), e / (1.0 + e))
+    return v * sig
+
+
+def swiglu_reference(x: np.ndarray, gate: tuple, up: tuple, group_size: int = 128) -> np.ndarray:
+    """h = silu(x @ Wg) * (x @ Wu) in float64 (engine/llama_mlp.py:30-32).
+
+    gate and up are (packed, scale) pairs; each product is fused_reference.
+    """
+    g = fused_reference(x, gate[0], gate[1], group_size)
+    u = fused_reference(x, up[0], up[1], group_size)
+    return silu(g) * u
 
 
 def cpu_path(x, packed, scale, group_size: int = 128):

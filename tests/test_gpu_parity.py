@@ -500,3 +500,130 @@ def test_lm_head_qwen3_8b_full_size():
     assert torch.isfinite(y).all()
     assert excess.max().item() <= 1e-3 * rms.item()
     del w
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU gate/up pair (w4a16_swiglu)
+#
+# Bar: max |h - h64| <= U * ulp_bf16(h64) + 1e-3 * RMS(h64), h64 the float64
+# oracle.  U = 1/2 for M <= 16 (epilogue on the fp32 sums, one bf16 rounding).
+# For larger M gate and up are rounded to bf16 before the epilogue, as in the
+# reference (engine/llama_mlp.py:30-32 rounds each linear output); the rounding
+# of g reaches h scaled by |g silu'(g) / silu(g)| <= 4 and the rounding of u
+# by 1, each at most 2^-9 relative, i.e. below ulp(h)/2 per unit, so U = 3.
+# ---------------------------------------------------------------------------
+
+def check_swiglu(h: torch.Tensor, h_ref: np.ndarray, m: int, label: str) -> None:
+    hv = h.float().cpu().numpy().astype(np.float64)
+    rms = float(np.sqrt(np.mean(h_ref ** 2)))
+    units = 0.5 if m <= 16 else 3.0
+    excess = np.abs(hv - h_ref) - units * ulp_bf16(h_ref)
+    say(f"  {label}: rms={rms:.4g} max(excess)/rms={excess.max() / rms:.3e}")
+    assert np.isfinite(hv).all(), label
+    assert excess.max() <= 1e-3 * rms, label
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1024, 1536), (2, 128, 512), (5, 512, 1000), (16, 2048, 768),
+                                   (17, 1024, 512), (32, 512, 1024), (33, 1024, 640), (200, 768, 1280)])
+def test_swiglu_vs_oracle(m, k, n):
+    from w4a16 import int4_swiglu, synth
+
+    say(f"swiglu m={m} k={k} n={n}")
+    gate = synth.make_weight(k, n, seed=70 + n)
+    up = synth.make_weight(k, n, seed=71 + n)
+    x = synth.make_activations(m, k, seed=72 + m)
+    h = int4_swiglu(x.to(DEV), *[(p.to(DEV), s.to(DEV)) for p, s in (gate, up)])
+    assert h.shape == (m, n) and h.dtype == torch.bfloat16
+    check_swiglu(h, orc.swiglu_reference(x.float().numpy(), gate, up), m, f"swiglu M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 24, 2048])
+def test_swiglu_qwen3_8b_full_size(m):
+    """gate/up of Qwen3-8B (K=4096, N=12288) against silu(g) * u from two
+    int4_matmul calls; M <= 16 also bit-stable over repeats (slots reset)."""
+    from w4a16 import int4_matmul, int4_swiglu, synth
+
+    say(f"swiglu full-size M={m}")
+    k, n = 4096, 12288
+    gate = synth.make_weight(k, n, seed=81, device=DEV)
+    up = synth.make_weight(k, n, seed=82, device=DEV)
+    x = synth.make_activations(m, k, seed=83, device=DEV)
+    h = int4_swiglu(x, gate, up)
+    g, u = int4_matmul(x, *gate).double(), int4_matmul(x, *up).double()
+    h_ref = (g * torch.sigmoid(g) * u).cpu().numpy()
+    # The reference-side g and u are themselves bf16-rounded: allow 3 ulp at every M.
+    hv = h.double().cpu().numpy()
+    rms = float(np.sqrt(np.mean(h_ref ** 2)))
+    excess = np.abs(hv - h_ref) - 3.0 * ulp_bf16(h_ref)
+    say(f"  vs two int4_matmul: max(excess)/rms={excess.max() / rms:.3e}")
+    assert excess.max() <= 1e-3 * rms
+    if m > 16:
+        # Same bf16 gate/up as the separate calls: the epilogue alone differs.
+        # Same bf16 gate/up as the separate calls, so only the epilogue's
+        # fp32 arithmetic and final rounding differ: within one ulp.
+        want = (torch.nn.functional.silu(g.float()) * u.float()).double().cpu().numpy()
+        assert (np.abs(hv - want) <= ulp_bf16(want) + 1e-30).all()
+    else:
+        for _ in range(3):
+            assert torch.equal(int4_swiglu(x, gate, up), h)
+        # sampled columns against the float64 oracle
+        cols = torch.randperm(n, generator=torch.Generator().manual_seed(m))[:48].sort().values.to(DEV)
+        sub = [(p[:, cols].cpu().numpy(), s[:, cols].cpu().numpy()) for p, s in (gate, up)]
+        check_swiglu(h[:, cols], orc.swiglu_reference(x.float().cpu().numpy(), *sub), m, "fp64 oracle, 48 cols")
+
+
+def test_swiglu_shares_workspace_and_edge_cases():
+    """Interleaved swiglu / linear calls on one workspace stay bit-stable; empty
+    and K = 0 inputs; unaligned activations; shape mismatch raises."""
+    from w4a16 import int4_matmul, int4_swiglu
+
+    x1, g1, s1 = rand_problem(1, 4096, 12288, seed=11)
+    _, u1, t1 = rand_problem(1, 4096, 12288, seed=12)
+    x2, p2, q2 = rand_problem(64, 1024, 512, seed=13)
+    h0 = int4_swiglu(x1, (g1, s1), (u1, t1))
+    y0 = int4_matmul(x2, p2, q2)
+    y1 = int4_matmul(x1, g1, s1)
+    for _ in range(3):
+        assert torch.equal(int4_swiglu(x1, (g1, s1), (u1, t1)), h0)
+        assert torch.equal(int4_matmul(x2, p2, q2), y0)
+        assert torch.equal(int4_matmul(x1, g1, s1), y1)
+    e = int4_swiglu(torch.empty(0, 4096, dtype=torch.bfloat16, device=DEV), (g1, s1), (u1, t1))
+    assert e.shape == (0, 12288)
+    z = torch.empty(0, 64, dtype=torch.int8, device=DEV)
+    zs = torch.empty(0, 64, device=DEV)
+    h = int4_swiglu(torch.empty(3, 0, dtype=torch.bfloat16, device=DEV), (z, zs), (z, zs))
+    assert h.shape == (3, 64) and torch.count_nonzero(h) == 0
+    for m in (3, 40):
+        x, gp, gs = rand_problem(m, 512, 256, seed=20 + m)
+        _, up, us = rand_problem(m, 512, 256, seed=30 + m)
+        flat = torch.zeros(m * 512 + 1, dtype=torch.bfloat16, device=DEV)
+        xu = flat[1:].view(m, 512)
+        xu.copy_(x)
+        ref = orc.swiglu_reference(x.float().cpu().numpy(), (gp.cpu().numpy(), gs.cpu().numpy()),
+                                   (up.cpu().numpy(), us.cpu().numpy()))
+        check_swiglu(int4_swiglu(xu, (gp, gs), (up, us)), ref, m, f"unaligned M={m}")
+    with pytest.raises(ValueError):
+        int4_swiglu(x1, (g1, s1), (u1[:, :1024], t1[:, :1024]))
+
+
+def test_swiglu_mlp_layer_matches_unfused():
+    """swiglu_mlp with INT4 weights equals the reference composition
+    down(silu(gate(x)) * up(x)) to the bars above."""
+    from w4a16 import _Int4Weight, linear, swiglu_mlp, synth
+
+    k, n = 512, 768
+    ws = {}
+    for name, (kk, nn), seed in (("gate", (k, n), 1), ("up", (k, n), 2), ("down", (n, k), 3)):
+        p, s = synth.make_weight(kk, nn, seed=600 + seed, device=DEV)
+        ws[f"mlp.{name}_proj.weight"] = _Int4Weight(p, s, 128, (nn, kk))
+    for m in (1, 48):
+        x = synth.make_activations(2 * m, k, seed=610 + m, device=DEV).reshape(2, m, k)
+        out = swiglu_mlp(x, ws)
+        assert out.shape == (2, m, k)
+        g = linear(x, ws["mlp.gate_proj.weight"]).float()
+        u = linear(x, ws["mlp.up_proj.weight"]).float()
+        ref = linear((g * torch.sigmoid(g) * u).to(torch.bfloat16), ws["mlp.down_proj.weight"]).double()
+        rms = float(ref.pow(2).mean().sqrt())
+        err = float((out.double() - ref).abs().max())
+        say(f"  swiglu_mlp m={m}: max|d|/rms={err / rms:.3e}")
+        assert err <= 2e-2 * rms

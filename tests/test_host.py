@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(native_lib):
     assert set(names) == set(_native.EXPORTED_SYMBOLS), names
     for name in names:
         assert hasattr(native_lib, name), name
-    assert native_lib.w4a16_abi_version() == 4
+    assert native_lib.w4a16_abi_version() == 5
 
 
 def _linear(lib, *, x=1, ldx=4096, packed=1, ldp=4096, scale=1, lds=4096, y=1, ldy=4096, m=1, n=4096,
@@ -139,6 +139,42 @@ def test_workspace_planning(native_lib):
                 if b:
                     slots = half(b) // (m * n * 4)  # nsplit - 1, rounded down by the 256-B alignment
                     assert 1 <= slots + (1 if half(b) % (m * n * 4) else 0) <= (k // 128 + 3) // 4
+
+
+def test_swiglu_workspace_and_validation(native_lib):
+    from w4a16 import _native as nat
+
+    lib = native_lib
+    size = ctypes.c_size_t(0)
+
+    def ws(m, n, k):
+        assert lib.w4a16_workspace_size_swiglu(m, n, k, 128, ctypes.byref(size)) == nat.W4A16_OK
+        return size.value
+
+    assert ws(0, 12288, 4096) == 0
+    assert ws(4, 12288, 0) == 0
+    # M <= 16: 8-wave workgroups (the pair launches > 1000 4-wave ones), so 4 K
+    # splits; gate publishes all 4, up the first 3.
+    assert (ws(1, 12288, 4096) - 256) // 2 == (4 + 3) * 12288 * 4
+    # Larger M: bf16 up projection at the start of the upper half, GEMM scratch after it.
+    assert (ws(2048, 12288, 4096) - 256) // 2 == 2048 * 12288 * 2 + 32 * 2048 * 4
+    # 16 < M <= 32: the up intermediate sets the half, the skinny slots fit under it.
+    assert (ws(32, 12288, 4096) - 256) // 2 >= 32 * 12288 * 2
+    assert lib.w4a16_workspace_size_swiglu(1, 4096, 4096, 64, ctypes.byref(size)) == nat.W4A16_ERR_GROUP_SIZE
+
+    def call(m=1, n=12288, k=4096, x=1, gp=1, gs=1, up=1, us=1, h=1, ldh=12288, group=128, wsp=None, wsb=0):
+        return lib.w4a16_swiglu(x, k, gp, n, gs, n, up, n, us, n, h, ldh, m, n, k, group, wsp, wsb, None)
+
+    assert call(group=64) == nat.W4A16_ERR_GROUP_SIZE
+    assert call(k=200) == nat.W4A16_ERR_K_GROUP
+    assert call(m=-1) == nat.W4A16_ERR_SHAPE
+    assert call(ldh=100) == nat.W4A16_ERR_SHAPE
+    assert call(up=None) == nat.W4A16_ERR_NULL
+    assert call(us=None) == nat.W4A16_ERR_NULL
+    assert call(h=None) == nat.W4A16_ERR_NULL
+    assert call() == nat.W4A16_ERR_WORKSPACE
+    assert call(m=2048) == nat.W4A16_ERR_WORKSPACE
+    assert call(m=0, x=None, gp=None, gs=None, up=None, us=None, h=None) == nat.W4A16_OK
 
 
 def test_int4_matmul_rejects_host_tensors_and_bad_args():

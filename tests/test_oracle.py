@@ -181,3 +181,34 @@ def test_cpu_path_reference_bound_and_agreement():
     yb = ab.float().numpy().astype(np.float64) @ wb.astype(np.float64)
     err = np.abs(outb.float().numpy() - yb).max()
     assert err <= 2e-2 * np.sqrt(np.mean(yb ** 2)) + 1e-6
+
+
+def test_silu_closed_forms():
+    v = np.linspace(-30.0, 30.0, 601)
+    s = orc.silu(v)
+    assert orc.silu(np.array([0.0]))[0] == 0.0
+    # x*sigma(x) - (-x)*sigma(-x) = x*(sigma(x) + sigma(-x)) = x
+    np.testing.assert_allclose(s - orc.silu(-v), v, rtol=0, atol=1e-12)
+    # sigma(ln 3) = 3/4
+    assert abs(orc.silu(np.array([np.log(3.0)]))[0] - 0.75 * np.log(3.0)) < 1e-15
+    # limits: -> x for large x, -> 0 (from below) for very negative x, finite at +-1000
+    assert abs(orc.silu(np.array([40.0]))[0] - 40.0) < 1e-12
+    assert -1e-12 < orc.silu(np.array([-40.0]))[0] < 0
+    assert np.isfinite(orc.silu(np.array([-1000.0, 1000.0]))).all()
+
+
+def test_swiglu_reference_with_summing_up_weight():
+    """Up weight with every code 1 and scale 1 makes u the row sum of x, so
+    h = silu(x @ Wg) * sum(x) exactly; a swapped gate/up or a dropped silu fails."""
+    rng = np.random.default_rng(5)
+    k, n, m = 256, 24, 3
+    gp = rng.integers(-128, 128, (k // 2, n), dtype=np.int8)
+    gs = rng.uniform(0.001, 0.01, (k // 128, n)).astype(np.float32)
+    up = np.full((k // 2, n), 0x11, dtype=np.int8)
+    us = np.ones((k // 128, n), dtype=np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    h = orc.swiglu_reference(x, (gp, gs), (up, us))
+    g = orc.fused_reference(x, gp, gs)
+    want = g / (1.0 + np.exp(-g)) * x.astype(np.float64).sum(1, keepdims=True)
+    np.testing.assert_allclose(h, want, rtol=1e-12, atol=1e-12)
+    assert not np.allclose(h, orc.swiglu_reference(x, (up, us), (gp, gs)))
