@@ -264,7 +264,7 @@ def main() -> int:
 
     import torch
 
-    from w4a16 import _native, int4_matmul, int4_matmul_grouped, synth
+    from w4a16 import _native, int4_matmul, int4_matmul_grouped, int4_swiglu, synth
 
     _native.load_library()
     dev = torch.device("cuda:0")
@@ -291,15 +291,17 @@ def main() -> int:
                 outs.append(int4_matmul(xs[k], packed, scale))
         return outs
 
-    def fused_layer(w, x4096, x12288):
+    def fused_layer(w, x4096):
+        # q/k/v in one grouped launch, gate/up as one fused SwiGLU call whose
+        # output h feeds down.
         qkv = int4_matmul_grouped(x4096, [w[ix["q_proj"]], w[ix["k_proj"]], w[ix["v_proj"]]])
         o = int4_matmul(x4096, *w[ix["o_proj"]])
-        gu = int4_matmul_grouped(x4096, [w[ix["gate_proj"]], w[ix["up_proj"]]])
-        d = int4_matmul(x12288, *w[ix["down_proj"]])
-        return qkv + [o] + gu + [d]
+        h = int4_swiglu(x4096, w[ix["gate_proj"]], w[ix["up_proj"]])
+        d = int4_matmul(h, *w[ix["down_proj"]])
+        return qkv + [o, h, d]
 
     def fused_sweep():
-        return [fused_layer(weights[l], xs[4096], xs[12288]) for l in range(layers)]
+        return [fused_layer(weights[l], xs[4096]) for l in range(layers)]
 
     # ---- headline: drop-in sweep ----
     g_sweep, _ = capture(sweep, stream)
@@ -342,6 +344,11 @@ def main() -> int:
         gbs = synth.algorithmic_bytes(1, k, n) / (us * 1e-6) / 1e9
         per_proj[name] = {"us": round(us, 3), "GB/s": round(gbs, 1)}
         log(f"  {name:10s} K={k:5d} N={n:5d}: {us:7.2f} us/launch  {gbs:7.1f} GB/s")
+    us = time_launches(lambda: [int4_swiglu(xs[4096], weights[l % layers][ix["gate_proj"]],
+                                            weights[l % layers][ix["up_proj"]]) for l in range(LAUNCHES)], stream)
+    gbs = 2 * synth.algorithmic_bytes(1, 4096, 12288) / (us * 1e-6) / 1e9
+    per_proj["swiglu_gate_up"] = {"us": round(us, 3), "GB/s": round(gbs, 1)}
+    log(f"  swiglu gate+up     : {us:7.2f} us/launch  {gbs:7.1f} GB/s")
     roofline = roofline_decode(per_proj["gate_proj"]["us"])
 
     # ---- config 3: batched decode / verify ----
@@ -372,13 +379,19 @@ def main() -> int:
             tf = synth.algorithmic_flops(m, k, n) / (us * 1e-6) / 1e12
             proj[name] = {"us": round(us, 2), "TFLOP/s": round(tf, 1)}
             log(f"  prefill {name:10s}: {us:8.2f} us  {tf:7.1f} TFLOP/s")
+        us = time_launches(lambda: [int4_swiglu(xp[4096], weights[l % layers][ix["gate_proj"]],
+                                                weights[l % layers][ix["up_proj"]]) for l in range(LAUNCHES)],
+                           stream, reps=3)
+        tf = 2 * synth.algorithmic_flops(m, 4096, 12288) / (us * 1e-6) / 1e12
+        proj["swiglu_gate_up"] = {"us": round(us, 2), "TFLOP/s": round(tf, 1)}
+        log(f"  prefill swiglu    : {us:8.2f} us  {tf:7.1f} TFLOP/s")
         flops = sum(synth.algorithmic_flops(m, k, n) for _, k, n in shapes)
 
         def layer_fn():
             return [int4_matmul(xp[k], *weights[l][i]) for l in range(4) for i, (_, k, n) in enumerate(shapes)]
 
         def layer_fused():
-            return [fused_layer(weights[l], xp[4096], xp[12288]) for l in range(4)]
+            return [fused_layer(weights[l], xp[4096]) for l in range(4)]
 
         res = {}
         for tag, fn in (("drop_in", layer_fn), ("grouped", layer_fused)):
