@@ -249,6 +249,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-32b", action="store_true", help="skip the Qwen3-32B (config 5) lines")
     ap.add_argument("--kernels-only", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
@@ -411,10 +412,66 @@ def main() -> int:
         roof_pf = roofline_prefill(proj["gate_proj"]["us"])
         del xp
 
+    # ---- config 1: Qwen3-0.6B gate at M=1 (the reference's CPU-runnable case) ----
+    _, k1, n1 = synth.QWEN3_06B_GATE
+    w1 = [synth.make_weight(k1, n1, seed=60 + l, device=dev) for l in range(LAUNCHES)]
+    x1 = synth.make_activations(1, k1, seed=61, device=dev)
+    us = time_launches(lambda: [int4_matmul(x1, *w1[l]) for l in range(LAUNCHES)], stream)
+    config1 = {"workload": "qwen3-0.6b gate_proj M=1 K=1024 N=3072", "us": round(us, 3),
+               "GB/s": round(synth.algorithmic_bytes(1, k1, n1) / (us * 1e-6) / 1e9, 1)}
+    log(f"config 1 (0.6B gate M=1): {us:.2f} us/launch, {config1['GB/s']} GB/s")
+    del w1
+
+    # ---- config 5: Qwen3-32B, 64-layer M=1 sweep and one M=4096 prefill layer ----
+    config5 = None
+    if not args.no_32b:
+        del weights
+        torch.cuda.empty_cache()
+        shapes32 = synth.QWEN3_32B
+        t0 = time.perf_counter()
+        w32 = make_layers(synth.QWEN3_32B_LAYERS, shapes32, dev)
+        x32 = {k: synth.make_activations(1, k, seed=k, device=dev) for k in {k for _, k, _ in shapes32}}
+        torch.cuda.synchronize()
+        log(f"generated {len(w32)} Qwen3-32B layers in {time.perf_counter() - t0:.1f}s")
+        bytes32 = sum(synth.algorithmic_bytes(1, k, n) for _, k, n in shapes32) * len(w32)
+
+        def sweep32():
+            return [int4_matmul(x32[k], *w32[l][i]) for l in range(len(w32)) for i, (_, k, _) in enumerate(shapes32)]
+
+        g32, _ = capture(sweep32, stream)
+        for _ in range(2):
+            g32.replay()
+        ms32 = time_graph(g32, stream, max(3, args.steps // 2))
+        del g32
+        gbs32 = bytes32 / (ms32 * 1e-3) / 1e9
+        log(f"config 5 (32B M=1, {len(w32)} layers): {ms32:.3f} ms/step, {gbs32:.1f} GB/s")
+        config5 = {"decode_M1": {"layers": len(w32), "ms_per_step": round(ms32, 4), "GB/s": round(gbs32, 1),
+                                 "frac_of_hbm_peak": round(gbs32 / HBM_PEAK_GBS, 4), "bytes_per_step": bytes32}}
+        if not args.no_prefill:
+            m = 4096
+            xp32 = {k: synth.make_activations(m, k, seed=k + 2, device=dev) for k in {k for _, k, _ in shapes32}}
+
+            def layer32():
+                return [int4_matmul(xp32[k], *w32[0][i]) for i, (_, k, _) in enumerate(shapes32)]
+
+            g, _ = capture(layer32, stream)
+            g.replay()
+            ms = time_graph(g, stream, 3)
+            del g
+            fl = sum(synth.algorithmic_flops(m, k, n) for _, k, n in shapes32)
+            tf = fl / (ms * 1e-3) / 1e12
+            log(f"config 5 (32B M=4096 layer): {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
+            config5["prefill_M4096_layer"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+                                              "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+            del xp32
+        del w32
+        torch.cuda.empty_cache()
+
     # ---- CPU baseline: the reference's host path on one layer ----
     cpu = None
     if not args.no_cpu_baseline:
-        host_layer = [(name, k, n, p.cpu(), s.cpu()) for (name, k, n), (p, s) in zip(shapes, weights[0])]
+        host_layer = [(name, k, n, p.cpu(), s.cpu())
+                      for (name, k, n), (p, s) in zip(shapes, make_layers(1, shapes, dev)[0])]
         cpu = cpu_baseline(host_layer, args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
 
@@ -443,6 +500,8 @@ def main() -> int:
         "per_projection_M1": per_proj,
         "batched_decode": batched,
         "prefill": prefill,
+        "config1_qwen3_06b": config1,
+        "config5_qwen3_32b": config5,
         "roofline": roofline,
         "roofline_prefill": roof_pf,
         "cpu_baseline": cpu,
