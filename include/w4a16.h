@@ -109,9 +109,8 @@ int w4a16_linear(const void* x, int64_t ldx,
 /*
  * Several independent projections: up to W4A16_MAX_PROBLEMS problems, each
  * with its own M, activations, weights and output (problems may share x, e.g.
- * q/k/v or gate/up of a decoder block).  Problems with M <= 16 run in one
- * decode launch and problems with M > 32 in one GEMM launch; 16 < M <= 32
- * problems launch one at a time.  Same arithmetic and status codes as
+ * q/k/v or gate/up of a decoder block).  Problems with M <= 32 run in one
+ * decode launch and problems with M > 32 in one GEMM launch.  Same arithmetic and status codes as
  * w4a16_linear; the workspace must be at least w4a16_workspace_size_grouped()
  * for the same table.
  *
@@ -134,7 +133,7 @@ int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int g
  *
  * Replaces `silu(linear(x, gate)) * linear(x, up)` of the reference MLP
  * (engine/llama_mlp.py:30-32, engine/llama_moe.py:44), i.e. two int4_matmul
- * launches plus two elementwise kernels.  M <= 16 runs one decode launch that
+ * launches plus two elementwise kernels.  M <= 32 runs one decode launch that
  * streams both weights and applies the epilogue to the fp32 sums (the
  * reference rounds gate and up to bf16 first; results agree to bf16 rounding).
  * Larger M computes gate into h and up into workspace, then one elementwise

@@ -10,8 +10,7 @@
 // A launch processes a table of up to kMaxProblems independent projections
 // that share M (one problem for the drop-in int4_matmul; q/k/v or gate/up or
 // a set of MoE experts for grouped calls).  Kernels:
-//   gemv_kernel     M <= 16  (decode)                       HBM bound
-//   skinny_kernel   16 < M <= 32 (batched decode / verify)  HBM bound, one problem
+//   gemv_kernel     M <= 32  (decode, batched decode / verify)  HBM bound
 //   rowsum_kernel   per-(group,row) activation sums for gemm_kernel
 //   gemm_kernel     M > 32 (prefill)                        MFMA bound
 //   splitk_reduce_kernel  ordered sum of gemm_kernel's K-split partials
@@ -45,13 +44,13 @@ struct Problem {
   int64_t lds;
   uint16_t* y;         // bf16 [M, N], row stride ldy elements
   int64_t ldy;
-  float* part;         // gemm: split-K partials [nsplit][M][N]; gemv / skinny: published
+  float* part;         // gemm: split-K partials [nsplit][M][N]; gemv: published
                        // partial slots [nsplit - 1][M][N] (workspace, zero between calls)
   float* rowsum;       // gemm: 136 * row sums [K/128][M] (workspace, maybe shared)
   int M, N, K;
   int wg_begin;        // first workgroup of this problem in the launch grid
   int rs_begin;        // rowsum_kernel: first workgroup (-1: row sums shared with another problem)
-  int tiles_m, tiles_n;  // gemm tile grid; gemv/skinny: tiles_n = column strips
+  int tiles_m, tiles_n;  // gemm tile grid; gemv: tiles_n = column strips
   int nsplit, gps;     // K split: nsplit ranges of gps groups
   int red_begin;       // splitk_reduce_kernel: first workgroup of this problem
   int vec;             // bit 0: packed and scale rows 16-byte aligned; bit 1: x rows 16-byte
@@ -230,9 +229,10 @@ __device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split
 }
 
 // ---------------------------------------------------------------------------
-// Decode GEMV kernel (M <= 16): the HBM-bound path of batch-1 decode.
+// Decode GEMV kernel (M <= 32): the HBM-bound path of decode and of small
+// batches (M > 16 runs two 16-row M subtiles that share every unpacked weight).
 //
-// Lane mapping (shared with skinny_kernel): a wave owns 16*CPL output columns;
+// Lane mapping: a wave owns 16*CPL output columns;
 // lane l covers columns col0 = n0 + CPL*(l%16) .. +CPL and, inside each 32-row
 // K step, rows 8*(l/16) .. +8, i.e. four packed rows.  Per 128-row group a
 // lane issues 16 loads of CPL bytes (4 steps x 4 packed rows).  Column t of the
@@ -262,15 +262,20 @@ struct DecodeSlot {
 
 // One group of one wave: A[st] are the activation fragments of the group's 4
 // K steps (rows past M zero), d the group's packed weights and scales.
-template <int CPL>
-__device__ __forceinline__ void decode_group(const DecodeSlot<CPL>& d, const bf16x8_t (&A)[4],
-                                             f32x4_t (&total)[CPL]) {
+// MT 16-row M subtiles share every unpacked B fragment.
+template <int CPL, int MT>
+__device__ __forceinline__ void decode_group(const DecodeSlot<CPL>& d, const bf16x8_t (&A)[MT][4],
+                                             f32x4_t (&total)[MT][CPL]) {
   constexpr int WPR = CPL / 4;
   const bf16x8_t neg136 = as_bf16x8(u32x4_t{kBf16Neg136, kBf16Neg136, kBf16Neg136, kBf16Neg136});
-  f32x4_t cinit = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t cinit[MT];
 #pragma unroll
-  for (int st = 0; st < 4; ++st) cinit = mfma16(A[st], neg136, cinit);
-  f32x4_t acc[CPL];
+  for (int mt = 0; mt < MT; ++mt) {
+    cinit[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) cinit[mt] = mfma16(A[mt][st], neg136, cinit[mt]);
+  }
+  f32x4_t acc[MT][CPL];
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
 #pragma unroll
@@ -283,14 +288,17 @@ __device__ __forceinline__ void decode_group(const DecodeSlot<CPL>& d, const bf1
         const int t = wi * 4 + c4;
         const bf16x8_t B = as_bf16x8(u32x4_t{pair_dyn(pw[0], c4), pair_dyn(pw[1], c4),
                                              pair_dyn(pw[2], c4), pair_dyn(pw[3], c4)});
-        acc[t] = mfma16(A[st], B, st == 0 ? cinit : acc[t]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][t] = mfma16(A[mt][st], B, st == 0 ? cinit[mt] : acc[mt][t]);
       }
     }
   }
 #pragma unroll
-  for (int t = 0; t < CPL; ++t)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) total[t][r] = __builtin_fmaf(acc[t][r], d.s[t], total[t][r]);
+    for (int t = 0; t < CPL; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) total[mt][t][r] = __builtin_fmaf(acc[mt][t][r], d.s[t], total[mt][t][r]);
 }
 
 // One wave's share of a decode launch: the 128-row group g of problem P for
@@ -298,27 +306,33 @@ __device__ __forceinline__ void decode_group(const DecodeSlot<CPL>& d, const bf1
 // fragments: lane (lc, lk) holds x[lc, g*128 + 32*st + 8*lk .. +8].  FULL
 // launches load them unconditionally (lanes past M read row 0) and zero them
 // with a select, so no branch or wait sits before the weight loads.
-template <int CPL, bool FULL>
+template <int CPL, bool FULL, int MT>
 __device__ __forceinline__ void decode_wave(const Problem& P, int g, int col0, int lc, int lk, int M,
-                                            f32x4_t (&total)[CPL]) {
+                                            f32x4_t (&total)[MT][CPL]) {
   const int N = P.N;
   const int G = (uint32_t)P.K / kGroup;
-  bf16x8_t A[4];
-  const uint32_t keep = lc < M ? 0xffffffffu : 0u;
+  bf16x8_t A[MT][4];
   DecodeSlot<CPL> d;
-  if constexpr (FULL) {
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(P.x, (uint32_t)((size_t)P.ldx * 2 * M));
-    const uint32_t xoff = ((uint32_t)(lc < M ? lc : 0) * (uint32_t)P.ldx + (uint32_t)(g * kGroup + lk * 8)) * 2u;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + st * 64, 0, 0));
-      A[st] = as_bf16x8(v & keep);
+  for (int mt = 0; mt < MT; ++mt) {
+    const int row = lc + 16 * mt;
+    const uint32_t keep = row < M ? 0xffffffffu : 0u;
+    if constexpr (FULL) {
+      const __amdgpu_buffer_rsrc_t xrs = make_rsrc(P.x, (uint32_t)((size_t)P.ldx * 2 * M));
+      const uint32_t xoff = ((uint32_t)(row < M ? row : 0) * (uint32_t)P.ldx + (uint32_t)(g * kGroup + lk * 8)) * 2u;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const u32x4_t v =
+            __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + st * 64, 0, 0));
+        A[mt][st] = as_bf16x8(v & keep);
+      }
+    } else {
+      const bool vec_x = (P.vec & 2) != 0;
+      const uint16_t* xrow = P.x + (int64_t)(row < M ? row : 0) * P.ldx + (int64_t)g * kGroup + lk * 8;
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        A[mt][st] = as_bf16x8(__builtin_bit_cast(u32x4_t, load_x8(xrow + st * 32, vec_x)) & keep);
     }
-  } else {
-    const bool vec_x = (P.vec & 2) != 0;
-    const uint16_t* xrow = P.x + (int64_t)(lc < M ? lc : 0) * P.ldx + (int64_t)g * kGroup + lk * 8;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) A[st] = as_bf16x8(__builtin_bit_cast(u32x4_t, load_x8(xrow + st * 32, vec_x)) & keep);
   }
   if constexpr (FULL) {
     const uint32_t ldp = (uint32_t)P.ldp;
@@ -350,8 +364,7 @@ __device__ __forceinline__ void decode_wave(const Problem& P, int g, int col0, i
   }
   // Everything above is in flight before the first MFMA below.
   __builtin_amdgcn_sched_barrier(0);
-  W4A16_MARK(1);
-  decode_group<CPL>(d, A, total);
+  decode_group<CPL, MT>(d, A, total);
 }
 
 // MULTI: the launch holds several problems.  A single-problem launch reads its
@@ -398,24 +411,30 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
   const bool active = wave < P.gps && g < G;  // wave-uniform
   W4A16_MARK(0);
 
-  f32x4_t total[CPL];
+  constexpr int MT = MROWS > 16 ? 2 : 1;
+  f32x4_t total[MT][CPL];
 #pragma unroll
-  for (int t = 0; t < CPL; ++t) total[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  if (active) decode_wave<CPL, FULL>(P, g, col0, lc, lk, M, total);
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) total[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if (active) decode_wave<CPL, FULL, MT>(P, g, col0, lc, lk, M, total);
   W4A16_MARK(3);
 
-  // Reduce the waves through LDS.  Rows m = 4*lk + r of the MFMA output.
+  // Reduce the waves through LDS.  Rows m = 16*mt + 4*lk + r of the MFMA output.
   float* red = smem;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = lk * 4 + r;
-    if (m < M) {
-      float* dst = red + ((size_t)wave * M + m) * WCOLS + lc * CPL;
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int t = 0; t < CPL; t += 4)
-        *reinterpret_cast<f32x4_t*>(dst + t) = f32x4_t{total[t][r], total[t + 1][r], total[t + 2][r], total[t + 3][r]};
+    for (int r = 0; r < 4; ++r) {
+      const int m = mt * 16 + lk * 4 + r;
+      if (m < M) {
+        float* dst = red + ((size_t)wave * M + m) * WCOLS + lc * CPL;
+#pragma unroll
+        for (int t = 0; t < CPL; t += 4)
+          *reinterpret_cast<f32x4_t*>(dst + t) =
+              f32x4_t{total[mt][t][r], total[mt][t + 1][r], total[mt][t + 2][r], total[mt][t + 3][r]};
+      }
     }
-  }
   __syncthreads();
   W4A16_MARK(4);
   const int elems = M * WCOLS;
@@ -443,140 +462,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
   }
   splitk_finish<NT, EPT, kFinishStore>(P, M, split, n0, WCOLS, M, wave_sum);
   W4A16_MARK(6);
-}
-
-// ---------------------------------------------------------------------------
-// Skinny kernel (16 < M <= 32, one problem).  Lane mapping and arithmetic as
-// gemv_kernel with two 16-row M subtiles sharing each unpacked B fragment;
-// activations come straight from global memory (rows past M zeroed by a
-// select), and the 4 waves of a workgroup take the split's groups round-robin.
-// ---------------------------------------------------------------------------
-constexpr int kSkinnyCPL = 8;
-
-struct SkinnyGroup {
-  uint32_t raw[4][4][kSkinnyCPL / 4];
-  bf16x8_t A[2][4];  // [M subtile][K step]
-  float s[kSkinnyCPL];
-};
-
-template <bool FULL>
-__device__ __forceinline__ void skinny_load(const Problem& P, int M, int g, int col0, int lc, int lk, SkinnyGroup& d) {
-  const bool vec_x = (P.vec & 2) != 0;
-#pragma unroll
-  for (int st = 0; st < 4; ++st)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
-      load_packed<kSkinnyCPL, FULL>(P.packed + pr * P.ldp, col0, P.N, (P.vec & 1) != 0, d.raw[st][r]);
-    }
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int m = lc + 16 * mt;
-    const int mrow = m < M ? m : M - 1;
-    const uint32_t keep = m < M ? 0xffffffffu : 0u;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const u32x4_t v = __builtin_bit_cast(
-          u32x4_t, load_x8(P.x + (int64_t)mrow * P.ldx + (int64_t)g * kGroup + st * 32 + lk * 8, vec_x));
-      d.A[mt][st] = as_bf16x8(v & keep);
-    }
-  }
-  load_scales<kSkinnyCPL, FULL>(P.scale + (int64_t)g * P.lds, col0, P.N, (P.vec & 1) != 0, d.s);
-}
-
-__device__ __forceinline__ void skinny_compute(const SkinnyGroup& d, f32x4_t (&total)[2][kSkinnyCPL]) {
-  constexpr int WPR = kSkinnyCPL / 4;
-  const bf16x8_t neg136 = as_bf16x8(u32x4_t{kBf16Neg136, kBf16Neg136, kBf16Neg136, kBf16Neg136});
-  f32x4_t cinit[2];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < 4; ++st) c = mfma16(d.A[mt][st], neg136, c);
-    cinit[mt] = c;
-  }
-  f32x4_t acc[2][kSkinnyCPL];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-#pragma unroll
-    for (int wi = 0; wi < WPR; ++wi) {
-      Prep pw[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pw[r] = prep(d.raw[st][r][wi]);
-#pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) {
-        const int t = wi * 4 + c4;
-        const bf16x8_t B = as_bf16x8(u32x4_t{pair_dyn(pw[0], c4), pair_dyn(pw[1], c4),
-                                             pair_dyn(pw[2], c4), pair_dyn(pw[3], c4)});
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) acc[mt][t] = mfma16(d.A[mt][st], B, st == 0 ? cinit[mt] : acc[mt][t]);
-      }
-    }
-  }
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int t = 0; t < kSkinnyCPL; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) total[mt][t][r] = __builtin_fmaf(acc[mt][t][r], d.s[t], total[mt][t][r]);
-}
-
-template <bool FULL>
-__global__ __launch_bounds__(256) void skinny_kernel(Launch L) {
-  constexpr int WCOLS = 16 * kSkinnyCPL;
-  extern __shared__ __attribute__((aligned(16))) float smem[];  // [4 waves][M][WCOLS]
-  const Problem& P = L.p[0];
-  const int strip = blockIdx.x % P.tiles_n;
-  const int split = blockIdx.x / P.tiles_n;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int lc = lane & 15;
-  const int lk = lane >> 4;
-  const int n0 = strip * WCOLS;
-  const int col0 = n0 + lc * kSkinnyCPL;
-  const int M = P.M, N = P.N;
-  const int G = P.K / kGroup;
-  const int g_begin = split * P.gps;
-  const int g_end = min(G, g_begin + P.gps);
-
-  f32x4_t total[2][kSkinnyCPL];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int t = 0; t < kSkinnyCPL; ++t) total[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int g = g_begin + wave; g < g_end; g += 4) {
-    SkinnyGroup cur;
-    skinny_load<FULL>(P, M, g, col0, lc, lk, cur);
-    skinny_compute(cur, total);
-  }
-
-  float* red = smem;
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = mt * 16 + lk * 4 + r;
-      if (m < M) {
-        float* dst = red + ((size_t)wave * M + m) * WCOLS + lc * kSkinnyCPL;
-#pragma unroll
-        for (int t = 0; t < kSkinnyCPL; t += 4)
-          *reinterpret_cast<f32x4_t*>(dst + t) =
-              f32x4_t{total[mt][t][r], total[mt][t + 1][r], total[mt][t + 2][r], total[mt][t + 3][r]};
-      }
-    }
-  __syncthreads();
-  const int elems = M * WCOLS;
-  auto wave_sum = [&](int e) {
-    return ((red[e] + red[(size_t)elems + e]) + red[(size_t)2 * elems + e]) + red[(size_t)3 * elems + e];
-  };
-  if (P.nsplit == 1) {
-    for (int e = threadIdx.x; e < elems; e += 256) {
-      const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
-      if (n < N) P.y[(int64_t)m * P.ldy + n] = f32_to_bf16(wave_sum(e));
-    }
-    return;
-  }
-  splitk_finish<256, 32 * WCOLS / 256, kFinishStore>(P, M, split, n0, WCOLS, M, wave_sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -1144,7 +1029,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(uint16_t* __restrict__ h,
 // ---------------------------------------------------------------------------
 // Host-side planning.
 // ---------------------------------------------------------------------------
-enum Kind { kGemv = 0, kSkinny = 1, kGemm = 2 };
+enum Kind { kGemv = 0, kGemm = 1 };
 
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1166,7 +1051,7 @@ struct Plan {
   bool full;           // every problem takes the unconditional (aligned, full tile) load path
   bool pair;           // SwiGLU pair (gemv only): problem 0 gate, problem 1 up
   size_t skip;         // bytes at the start of the upper workspace half reserved by the caller
-  size_t lds_bytes;    // dynamic LDS (gemv / skinny)
+  size_t lds_bytes;    // dynamic LDS (gemv)
   size_t ws_bytes;     // bytes of the plan's workspace half (see bind())
   int total_wgs;
   int rs_wgs;          // rowsum_kernel workgroups
@@ -1189,10 +1074,10 @@ int check_problem(const w4a16_problem& q) {
 
 bool gemm_x_ok(const w4a16_problem& q) { return aligned(q.x, 16) && q.ldx % 8 == 0; }
 
-inline Kind kind_of(int M) { return M <= 16 ? kGemv : (M <= 32 ? kSkinny : kGemm); }
+inline Kind kind_of(int M) { return M <= 32 ? kGemv : kGemm; }
 
 // Plan one launch over problems that all have M > 0, N > 0, K > 0 and the
-// same kind (kind_of(M)); the skinny kernel takes a single problem.
+// same kind (kind_of(M)).
 Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
   Plan pl{};
   pl.pair = pair;
@@ -1224,12 +1109,13 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
   }
 
   size_t ws = 0;
-  if (pl.kind == kGemv || pl.kind == kSkinny) {
+  if (pl.kind == kGemv) {
     // Decode shape choice (measured over the Qwen3-8B / 32B projections at
-    // M = 1..16 on MI355X):
+    // M = 1..32 on MI355X):
     //  * 128-column strips (CPL 8), or 64-column strips (CPL 4) when N is not
-    //    a multiple of 128 or 128-column strips would give the launch fewer
-    //    than 128 workgroups (k/v projections: more, smaller workgroups);
+    //    a multiple of 128, when 128-column strips would give the launch fewer
+    //    than 128 workgroups (k/v projections: more, smaller workgroups), or
+    //    when M > 16 (two M subtiles: 103 instead of 140 VGPRs per lane);
     //  * 4 waves per workgroup (one 128-row group each), or 8 when M >= 8,
     //    when 4 would launch more than 1000 workgroups, or split K more than
     //    20 ways: past that, reducing inside the workgroup beats more splits.
@@ -1241,13 +1127,12 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
       max_split4 = std::max(max_split4, ceil_div(G, 4));
       n_odd += probs[i].N % 128 != 0;
     }
-    int cpl = kSkinnyCPL;
-    if (pl.kind == kGemv) cpl = env_int("W4A16_CPL", (n_odd > 0 || wg8 < 128) ? 4 : 8);
+    const int cpl = env_int("W4A16_CPL", (n_odd > 0 || wg8 < 128 || max_m > 16) ? 4 : 8);
     pl.cpl = cpl;
     const int wcols = 16 * cpl;
     int wg4 = 0;
     for (int i = 0; i < count; ++i) wg4 += ceil_div(probs[i].N, wcols) * ceil_div(probs[i].K / kGroup, 4);
-    pl.waves = (pl.kind == kGemv && (max_m >= 8 || wg4 > 1000 || max_split4 > 20)) ? 8 : 4;
+    pl.waves = (max_m >= 8 || wg4 > 1000 || max_split4 > 20) ? 8 : 4;
     pl.waves = env_int("W4A16_WAVES", pl.waves);
     int wg = 0;
     size_t lds = 0;
@@ -1257,27 +1142,15 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
       const int M = P.M;
       P.tiles_m = 1;
       P.tiles_n = ceil_div(P.N, wcols);
-      if (pl.kind == kGemv) {
-        P.gps = pl.waves;  // one 128-row group per wave
-        P.nsplit = ceil_div(G, P.gps);
-        lds = std::max(lds, (size_t)pl.waves * M * wcols * 4);
-      } else {
-        // Split K until ~2 workgroups per CU, keeping at least one group per
-        // wave and the fp32 partial traffic within a quarter of the weights.
-        int nsplit = ceil_div(512, P.tiles_n);
-        const int by_traffic = std::max(1, (int)((int64_t)P.K / (64 * (int64_t)M)));
-        nsplit = std::min(nsplit, std::min(by_traffic, ceil_div(G, 4)));
-        nsplit = std::max(1, nsplit);
-        P.gps = ceil_div(G, nsplit);
-        P.nsplit = ceil_div(G, P.gps);
-        lds = std::max(lds, (size_t)4 * M * wcols * 4);
-      }
+      P.gps = pl.waves;  // one 128-row group per wave
+      P.nsplit = ceil_div(G, P.gps);
+      lds = std::max(lds, (size_t)pl.waves * M * wcols * 4);
       P.wg_begin = wg;
       wg += P.tiles_n * P.nsplit;
       const size_t wbytes = (size_t)(P.K / 2) * P.ldp, sbytes = (size_t)G * P.lds * 4;
       const size_t xbytes = (size_t)P.ldx * 2 * M;
-      full = full && (P.vec & 1) && P.N % wcols == 0 && wbytes < 0xffffffffull && sbytes < 0xffffffffull;
-      if (pl.kind == kGemv) full = full && (P.vec & 2) && xbytes < 0xffffffffull;
+      full = full && (P.vec & 1) && (P.vec & 2) && P.N % wcols == 0 && wbytes < 0xffffffffull &&
+             sbytes < 0xffffffffull && xbytes < 0xffffffffull;
       // Published slots: nsplit - 1 per strip (the last split finishes), all
       // nsplit for the gate of a pair (up's finisher reads them).
       const int nslots = pair && i == 0 ? P.nsplit : P.nsplit - 1;
@@ -1389,7 +1262,8 @@ void launch_gemv_as(const Plan& pl, dim3 grid, hipStream_t s) {
   if (pl.full)
     hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, true, MULTI, MROWS, PAIR>), grid, block, pl.lds_bytes, s, pl.L);
   else
-    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, false, MULTI, 16, PAIR>), grid, block, pl.lds_bytes, s, pl.L);
+    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, false, MULTI, (MROWS > 16 ? 32 : 16), PAIR>), grid, block,
+                       pl.lds_bytes, s, pl.L);
 }
 
 template <int CPL, int WAVES, bool MULTI, bool PAIR = false>
@@ -1400,8 +1274,10 @@ void launch_gemv_rows(const Plan& pl, dim3 grid, int max_m, hipStream_t s) {
     launch_gemv_as<CPL, WAVES, MULTI, 4, PAIR>(pl, grid, s);
   else if (max_m <= 8)
     launch_gemv_as<CPL, WAVES, MULTI, 8, PAIR>(pl, grid, s);
-  else
+  else if (max_m <= 16)
     launch_gemv_as<CPL, WAVES, MULTI, 16, PAIR>(pl, grid, s);
+  else
+    launch_gemv_as<CPL, WAVES, MULTI, 32, PAIR>(pl, grid, s);
 }
 
 template <int CPL, int WAVES>
@@ -1432,11 +1308,11 @@ int launch_gemm(const Plan& pl, hipStream_t s) {
 bool separate(const w4a16_problem& q) { return q.K == 0 || (q.M > 32 && !gemm_x_ok(q)); }
 
 // The launches of one call: problems with M > 0 and N > 0 grouped by kernel.
-// Each decode (M <= 16) and GEMM group is one launch; skinny problems
-// (16 < M <= 32) launch one at a time.  Problems in `sep` are handled alone.
+// The decode (M <= 32) and the GEMM group are one launch each.  Problems in
+// `sep` are handled alone.
 struct Batches {
-  w4a16_problem gemv[kMaxProblems], gemm[kMaxProblems], skinny[kMaxProblems], sep[kMaxProblems];
-  int n_gemv = 0, n_gemm = 0, n_skinny = 0, n_sep = 0;
+  w4a16_problem gemv[kMaxProblems], gemm[kMaxProblems], sep[kMaxProblems];
+  int n_gemv = 0, n_gemm = 0, n_sep = 0;
 };
 
 Batches split(const w4a16_problem* probs, int count) {
@@ -1448,16 +1324,15 @@ Batches split(const w4a16_problem* probs, int count) {
       b.sep[b.n_sep++] = q;
       continue;
     }
-    switch (kind_of(q.M)) {
-      case kGemv: b.gemv[b.n_gemv++] = q; break;
-      case kSkinny: b.skinny[b.n_skinny++] = q; break;
-      default: b.gemm[b.n_gemm++] = q; break;
-    }
+    if (kind_of(q.M) == kGemv)
+      b.gemv[b.n_gemv++] = q;
+    else
+      b.gemm[b.n_gemm++] = q;
   }
   return b;
 }
 
-// Unaligned activations with M > 32 go through the skinny kernel 32 rows at a time.
+// Unaligned activations with M > 32 go through the decode kernel 32 rows at a time.
 template <class Fn>
 int for_each_chunk(const w4a16_problem& q, Fn fn) {
   for (int m0 = 0; m0 < q.M; m0 += 32) {
@@ -1482,13 +1357,6 @@ int launch_plan(const w4a16_problem* probs, int count, void* workspace, size_t w
   if (pl.kind == kGemv) {
     if (pl.waves == 8) return pl.cpl == 4 ? launch_gemv<4, 8>(pl, s) : launch_gemv<8, 8>(pl, s);
     return pl.cpl == 4 ? launch_gemv<4, 4>(pl, s) : launch_gemv<8, 4>(pl, s);
-  }
-  if (pl.kind == kSkinny) {
-    if (pl.full)
-      hipLaunchKernelGGL(skinny_kernel<true>, dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
-    else
-      hipLaunchKernelGGL(skinny_kernel<false>, dim3(pl.total_wgs), dim3(256), pl.lds_bytes, s, pl.L);
-    return launch_status();
   }
   hipLaunchKernelGGL(rowsum_kernel, dim3(pl.rs_wgs), dim3(256), 0, s, pl.L);
   const int rc = launch_status();
@@ -1529,10 +1397,6 @@ int run(const w4a16_problem* probs, int count, void* workspace, size_t workspace
     const int rc = launch_plan(b.gemv, b.n_gemv, workspace, workspace_bytes, s, skip);
     if (rc != W4A16_OK) return rc;
   }
-  for (int i = 0; i < b.n_skinny; ++i) {
-    const int rc = launch_plan(&b.skinny[i], 1, workspace, workspace_bytes, s, skip);
-    if (rc != W4A16_OK) return rc;
-  }
   if (b.n_gemm > 0) return launch_plan(b.gemm, b.n_gemm, workspace, workspace_bytes, s, skip);
   return W4A16_OK;
 }
@@ -1549,8 +1413,6 @@ int workspace_for(const w4a16_problem* probs, int count, size_t* bytes, size_t s
   }
   int rc = W4A16_OK;
   if (b.n_gemv > 0 && (rc = plan_workspace(b.gemv, b.n_gemv, bytes, skip)) != W4A16_OK) return rc;
-  for (int i = 0; i < b.n_skinny; ++i)
-    if ((rc = plan_workspace(&b.skinny[i], 1, bytes, skip)) != W4A16_OK) return rc;
   if (b.n_gemm > 0 && (rc = plan_workspace(b.gemm, b.n_gemm, bytes, skip)) != W4A16_OK) return rc;
   return W4A16_OK;
 }
@@ -1559,7 +1421,7 @@ int workspace_for(const w4a16_problem* probs, int count, size_t* bytes, size_t s
 // one decode launch whose finishers apply the epilogue to the fp32 sums.
 // Larger M: gate into h and up into the first `ubytes` of the upper workspace
 // half (one grouped launch), then silu_mul_kernel.
-size_t swiglu_up_bytes(int M, int N) { return M <= 16 ? 0 : align256((size_t)M * N * 2); }
+size_t swiglu_up_bytes(int M, int N) { return kind_of(M) == kGemv ? 0 : align256((size_t)M * N * 2); }
 
 int swiglu(const w4a16_problem pair[2], void* workspace, size_t workspace_bytes, hipStream_t s) {
   const w4a16_problem& g = pair[0];
@@ -1569,7 +1431,7 @@ int swiglu(const w4a16_problem pair[2], void* workspace, size_t workspace_bytes,
                        static_cast<uint16_t*>(g.y), g.ldy, g.M, g.N);
     return launch_status();
   }
-  if (g.M <= 16) return launch_plan(pair, 2, workspace, workspace_bytes, s, 0, true);
+  if (kind_of(g.M) == kGemv) return launch_plan(pair, 2, workspace, workspace_bytes, s, 0, true);
   const size_t ub = swiglu_up_bytes(g.M, g.N);
   if (!workspace || workspace_bytes < 2 * ub + 256) return W4A16_ERR_WORKSPACE;
   w4a16_problem q[2] = {pair[0], pair[1]};
@@ -1587,7 +1449,7 @@ int swiglu_workspace(const w4a16_problem pair[2], size_t* bytes) {
   *bytes = 0;
   const w4a16_problem& g = pair[0];
   if (g.M == 0 || g.N == 0 || g.K == 0) return W4A16_OK;
-  if (g.M <= 16) return plan_workspace(pair, 2, bytes, 0, true);
+  if (kind_of(g.M) == kGemv) return plan_workspace(pair, 2, bytes, 0, true);
   const size_t ub = swiglu_up_bytes(g.M, g.N);
   const int rc = workspace_for(pair, 2, bytes, ub);
   *bytes = std::max(*bytes, 2 * ub + 256);

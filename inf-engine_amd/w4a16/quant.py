@@ -127,7 +127,7 @@ def int4_matmul_grouped(a, weights, group_size: int = 128) -> list[torch.Tensor]
     ``a`` is one ``(M, K)`` bf16 tensor shared by every projection (q/k/v or
     gate/up of a block) or a list of per-projection activations, each with its
     own M (a set of MoE experts with their token counts).  ``weights`` is a list
-    of ``(packed, scale)`` pairs, at most 16.  Projections with M <= 16 share one
+    of ``(packed, scale)`` pairs, at most 16.  Projections with M <= 32 share one
     decode launch and those with M > 32 one GEMM launch.  Results equal
     ``int4_matmul`` on each pair up to fp32 summation order.  No reference
     counterpart: the reference calls ``int4_matmul`` once per projection
@@ -169,7 +169,7 @@ def int4_swiglu(a: torch.Tensor, gate, up, group_size: int = 128) -> torch.Tenso
     ``gate`` and ``up`` are ``(packed, scale)`` pairs of the same shape.  The
     reference computes ``silu(linear(x, gate)) * linear(x, up)``
     (engine/llama_mlp.py:30-32, engine/llama_moe.py:44) as two int4_matmul
-    launches and two elementwise kernels; here M <= 16 is a single decode
+    launches and two elementwise kernels; here M <= 32 is a single decode
     launch with the epilogue on the fp32 sums, larger M the grouped GEMM plus
     one elementwise pass.  Same checks and exceptions as ``int4_matmul``.
     """

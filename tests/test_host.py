@@ -158,8 +158,8 @@ def test_swiglu_workspace_and_validation(native_lib):
     assert (ws(1, 12288, 4096) - 256) // 2 == (4 + 3) * 12288 * 4
     # Larger M: bf16 up projection at the start of the upper half, GEMM scratch after it.
     assert (ws(2048, 12288, 4096) - 256) // 2 == 2048 * 12288 * 2 + 32 * 2048 * 4
-    # 16 < M <= 32: the up intermediate sets the half, the skinny slots fit under it.
-    assert (ws(32, 12288, 4096) - 256) // 2 >= 32 * 12288 * 2
+    # M <= 32 is still one decode launch: 4 + 3 slots of [32, N].
+    assert (ws(32, 12288, 4096) - 256) // 2 == (4 + 3) * 32 * 12288 * 4
     assert lib.w4a16_workspace_size_swiglu(1, 4096, 4096, 64, ctypes.byref(size)) == nat.W4A16_ERR_GROUP_SIZE
 
     def call(m=1, n=12288, k=4096, x=1, gp=1, gs=1, up=1, us=1, h=1, ldh=12288, group=128, wsp=None, wsb=0):
