@@ -411,7 +411,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
   const bool active = wave < P.gps && g < G;  // wave-uniform
   W4A16_MARK(0);
 
-  constexpr int MT = MROWS > 16 ? 2 : 1;
+  constexpr int MT = (MROWS + 15) / 16;
   f32x4_t total[MT][CPL];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -553,14 +553,15 @@ __device__ __forceinline__ void gemm_unpack(const uint32_t (&raw)[4], bf16x8_t (
   }
 }
 
-template <int CPL, bool FULL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void gemm_kernel(Launch L) {
+template <int CPL, bool FULL, int KW>
+__global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))) void gemm_kernel(Launch L) {
   constexpr int WCOLS = 16 * CPL;       // columns per wave
+  constexpr int kATile = 4 * kGemmMT * 64;  // 16-byte entries of one activation tile
   // Two activation buffers [step][subtile][lane] (16 B each) and two row-sum
-  // buffers, as separate objects so that alias analysis can tell a copy into
-  // one from a read of the other.
-  __shared__ u32x4_t As0[4 * kGemmMT * 64], As1[4 * kGemmMT * 64];
-  __shared__ __attribute__((aligned(16))) float Cs0[kGemmRows], Cs1[kGemmRows];
+  // buffers per K half, as separate objects so that alias analysis can tell a
+  // copy into one from a read of the other.
+  __shared__ u32x4_t As0[KW * kATile], As1[KW * kATile];
+  __shared__ __attribute__((aligned(16))) float Cs0[KW * kGemmRows], Cs1[KW * kGemmRows];
   auto a_buf = [&](auto tag) -> u32x4_t* {
     if constexpr (decltype(tag)::value == 0) return As0; else return As1;
   };
@@ -590,7 +591,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   const int n_tile = in_band / band_rows;
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x & 255) >> 6);  // column block
+  const int kw = KW == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8);  // K half
   const int lc = lane & 15;
   const int lk = lane >> 4;
   const int M = P.M, N = P.N;
@@ -623,8 +625,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   const uint32_t cv = (uint32_t)min(m0 + (int)(threadIdx.x & 127), M - 1) * 4u;
 
   auto stage_a = [&](int g, auto buf_tag) {
-    u32x4_t* as = a_buf(buf_tag);
-    float* cs = c_buf(buf_tag);
+    u32x4_t* as = a_buf(buf_tag) + kw * kATile;
+    float* cs = c_buf(buf_tag) + kw * kGemmRows;
 #pragma unroll
     for (int i = 0; i < kGemmMT; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (void __attribute__((address_space(3)))*)&as[(wave * kGemmMT + i) * 64],
@@ -685,14 +687,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   // Packed weights (4 K steps) and scales of two groups: the group computed
   // from set BUF while the next one loads into set BUF ^ 1 (the same
   // compile-time ping-pong as the LDS buffers, so no register copies).
+  // With KW == 2 the two K halves of the workgroup (waves 0-3 and 4-7) take
+  // alternate groups of the range, each with its own LDS buffers, and are
+  // summed through LDS at the end.
   uint32_t raw2[2][4][4];
   float s2[2][CPL];
   float s_ref[CPL];  // scale U is currently expressed in (per column)
-  load_b(g_begin, raw2[0], s2[0]);
-  stage_a(g_begin, std::integral_constant<int, 0>{});
-  W4A16_MARK(1);
+  const int g_first = g_begin + kw;
+  const int n_iter = (g_end - g_begin + KW - 1) / KW;  // iterations of every K half (barrier count)
 #pragma unroll
-  for (int t = 0; t < CPL; ++t) s_ref[t] = clamp_scale(s2[0][t]);
+  for (int t = 0; t < CPL; ++t) s_ref[t] = 1.f;
+  if (g_first < g_end) {
+    load_b(g_first, raw2[0], s2[0]);
+    stage_a(g_first, std::integral_constant<int, 0>{});
+  }
+  W4A16_MARK(1);
+  if (g_first < g_end) {
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) s_ref[t] = clamp_scale(s2[0][t]);
+  }
 
   // One group.  BUF is the LDS buffer holding this group's activations; the
   // next group is staged into the other one.  BUF is a compile-time constant
@@ -700,21 +713,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   // direct-to-LDS copies into buffer BUF ^ 1 from the reads of buffer BUF:
   // with a run-time index it must assume they alias and waits for the copies
   // (vmcnt(0)) before the first LDS read, which serializes the prefetch.
-  auto group = [&](auto buf_tag, int g) {
+  auto group = [&](auto buf_tag, int it) {
     constexpr int b = decltype(buf_tag)::value;
-    const u32x4_t* as = a_buf(buf_tag);
-    const float* cs = c_buf(buf_tag);
+    const int g = g_first + it * KW;
+    const u32x4_t* as = a_buf(buf_tag) + kw * kATile;
+    const float* cs = c_buf(buf_tag) + kw * kGemmRows;
     uint32_t (&raw)[4][4] = raw2[b];
     const float (&s)[CPL] = s2[b];
     // Direct-to-LDS copies of this group (issued one iteration earlier) must
     // have landed before the barrier publishes them.
     wait_vmem();
     __syncthreads();
+    if (g >= g_end) return;  // the K half with one group less: barriers only
 
-    const bool has_next = g + 1 < g_end;
+    const bool has_next = g + KW < g_end;
     if (has_next) {
-      stage_a(g + 1, std::integral_constant<int, b ^ 1>{});
-      load_b(g + 1, raw2[b ^ 1], s2[b ^ 1]);
+      stage_a(g + KW, std::integral_constant<int, b ^ 1>{});
+      load_b(g + KW, raw2[b ^ 1], s2[b ^ 1]);
     }
 
     // Fold: U <- U * (s_ref / s) - 136 * rowsum.  (U is zero before the first
@@ -780,9 +795,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       if constexpr (kStepPrio) __builtin_amdgcn_s_setprio(0);
     }
   };
-  for (int g = g_begin; g < g_end; g += 2) {
-    group(std::integral_constant<int, 0>{}, g);
-    if (g + 1 < g_end) group(std::integral_constant<int, 1>{}, g + 1);
+  for (int it = 0; it < n_iter; it += 2) {
+    group(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < n_iter) group(std::integral_constant<int, 1>{}, it + 1);
+  }
+
+  if constexpr (KW == 2) {
+    // K half 1 hands its scaled tile to half 0 through the (now idle)
+    // activation buffers: subtiles 0-3 in As0, 4-7 in As1, fragment order.
+    __syncthreads();
+    if (kw == 1) {
+#pragma unroll
+      for (int i = 0; i < kGemmMT; ++i)
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) {
+          f32x4_t v;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = U[i][t][r] * s_ref[t];
+          u32x4_t* dst = i < kGemmMT / 2 ? As0 : As1;
+          dst[((wave * (kGemmMT / 2) + (i % (kGemmMT / 2))) * CPL + t) * 64 + lane] = __builtin_bit_cast(u32x4_t, v);
+        }
+    }
+    __syncthreads();
+    if (kw == 1) return;
+#pragma unroll
+    for (int i = 0; i < kGemmMT; ++i)
+#pragma unroll
+      for (int t = 0; t < CPL; ++t) {
+        const u32x4_t* src = i < kGemmMT / 2 ? As0 : As1;
+        const f32x4_t o = __builtin_bit_cast(
+            f32x4_t, src[((wave * (kGemmMT / 2) + (i % (kGemmMT / 2))) * CPL + t) * 64 + lane]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) U[i][t][r] = __builtin_fmaf(U[i][t][r], s_ref[t], o[r]);
+      }
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) s_ref[t] = 1.f;
   }
 
   // ---- output: lane holds rows m0 + 16i + 4lk + r, columns col0 .. col0+CPL-1 ----
@@ -1048,6 +1095,7 @@ struct Plan {
   Kind kind;
   int cpl;
   int waves;           // gemv: waves per workgroup (4 or 8)
+  int kw;              // gemm: K halves per workgroup (1, or 2 with 8 waves)
   bool full;           // every problem takes the unconditional (aligned, full tile) load path
   bool pair;           // SwiGLU pair (gemv only): problem 0 gate, problem 1 up
   size_t skip;         // bytes at the start of the upper workspace half reserved by the caller
@@ -1074,7 +1122,10 @@ int check_problem(const w4a16_problem& q) {
 
 bool gemm_x_ok(const w4a16_problem& q) { return aligned(q.x, 16) && q.ldx % 8 == 0; }
 
-inline Kind kind_of(int M) { return M <= 32 ? kGemv : kGemm; }
+inline Kind kind_of(int M) {
+  static const int gemv_max = env_int("W4A16_GEMV_MAX", 32);
+  return M <= gemv_max ? kGemv : kGemm;
+}
 
 // Plan one launch over problems that all have M > 0, N > 0, K > 0 and the
 // same kind (kind_of(M)).
@@ -1162,10 +1213,18 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
     pl.lds_bytes = lds;
     pl.total_wgs = wg;
   } else {
-    // GEMM: 256-column tiles unless that leaves the chip under-filled.
+    // GEMM tile choice (measured on the Qwen3-8B / 32B shapes at M = 2048):
+    //  * 128 x 256 tiles when there are at least 192 of them, else 128 x 128
+    //    tiles with K split across workgroups;
+    //  * with at most 256 such tiles (one per CU), 8-wave workgroups whose two
+    //    K halves run side by side (KW 2): the CU still holds two waves per
+    //    SIMD (q/o 92.7 -> 77 us, down 266 -> 208 us); above 256 tiles two
+    //    4-wave workgroups per CU do better (32B down 674 vs 799 us).
     int t4 = 0;
     for (int i = 0; i < count; ++i) t4 += ceil_div(probs[i].M, kGemmRows) * ceil_div(probs[i].N, 256);
-    pl.cpl = env_int("W4A16_GCPL", t4 < 384 ? 2 : 4);
+    pl.cpl = env_int("W4A16_GCPL", t4 < 192 ? 2 : 4);
+    pl.kw = env_int("W4A16_GKW", pl.cpl == 4 && t4 <= 256 ? 2 : 1);
+    if (pl.cpl == 2) pl.kw = 1;
     const int tcols = 64 * pl.cpl;
     int tiles_total = 0;
     for (int i = 0; i < count; ++i) tiles_total += ceil_div(probs[i].M, kGemmRows) * ceil_div(probs[i].N, tcols);
@@ -1262,7 +1321,7 @@ void launch_gemv_as(const Plan& pl, dim3 grid, hipStream_t s) {
   if (pl.full)
     hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, true, MULTI, MROWS, PAIR>), grid, block, pl.lds_bytes, s, pl.L);
   else
-    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, false, MULTI, (MROWS > 16 ? 32 : 16), PAIR>), grid, block,
+    hipLaunchKernelGGL((gemv_kernel<CPL, WAVES, false, MULTI, (MROWS > 32 ? 64 : (MROWS > 16 ? 32 : 16)), PAIR>), grid, block,
                        pl.lds_bytes, s, pl.L);
 }
 
@@ -1276,6 +1335,10 @@ void launch_gemv_rows(const Plan& pl, dim3 grid, int max_m, hipStream_t s) {
     launch_gemv_as<CPL, WAVES, MULTI, 8, PAIR>(pl, grid, s);
   else if (max_m <= 16)
     launch_gemv_as<CPL, WAVES, MULTI, 16, PAIR>(pl, grid, s);
+#ifdef W4A16_EXP
+  else if (max_m > 32)
+    launch_gemv_as<CPL, WAVES, MULTI, 64, PAIR>(pl, grid, s);
+#endif
   else
     launch_gemv_as<CPL, WAVES, MULTI, 32, PAIR>(pl, grid, s);
 }
@@ -1293,13 +1356,13 @@ int launch_gemv(const Plan& pl, hipStream_t s) {
   return launch_status();
 }
 
-template <int CPL>
+template <int CPL, int KW>
 int launch_gemm(const Plan& pl, hipStream_t s) {
   const int grid = (pl.total_wgs + 7) & ~7;
   if (pl.full)
-    hipLaunchKernelGGL((gemm_kernel<CPL, true>), dim3(grid), dim3(256), 0, s, pl.L);
+    hipLaunchKernelGGL((gemm_kernel<CPL, true, KW>), dim3(grid), dim3(256 * KW), 0, s, pl.L);
   else
-    hipLaunchKernelGGL((gemm_kernel<CPL, false>), dim3(grid), dim3(256), 0, s, pl.L);
+    hipLaunchKernelGGL((gemm_kernel<CPL, false, KW>), dim3(grid), dim3(256 * KW), 0, s, pl.L);
   return launch_status();
 }
 
@@ -1361,7 +1424,7 @@ int launch_plan(const w4a16_problem* probs, int count, void* workspace, size_t w
   hipLaunchKernelGGL(rowsum_kernel, dim3(pl.rs_wgs), dim3(256), 0, s, pl.L);
   const int rc = launch_status();
   if (rc != W4A16_OK) return rc;
-  const int rc2 = pl.cpl == 2 ? launch_gemm<2>(pl, s) : launch_gemm<4>(pl, s);
+  const int rc2 = pl.cpl == 2 ? launch_gemm<2, 1>(pl, s) : (pl.kw == 2 ? launch_gemm<4, 2>(pl, s) : launch_gemm<4, 1>(pl, s));
   if (rc2 != W4A16_OK || pl.red_wgs == 0) return rc2;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(pl.red_wgs), dim3(256), 0, s, pl.L);
   return launch_status();

@@ -164,6 +164,20 @@ def test_tolerance_vs_oracle(m, k, n):
     check_tolerance(y, y_ref, f"M={m} K={k} N={n}")
 
 
+@pytest.mark.parametrize("m,k,n", [(1536, 384, 4000), (1536, 640, 4096), (1500, 128, 4096)])
+def test_gemm_two_k_halves(m, k, n):
+    """192..256 tiles of 128 x 256: one 8-wave workgroup per tile whose two K
+    halves are summed in LDS.  Odd group counts leave one half a group short
+    (K=384, 640), K=128 leaves one half empty, N=4000 takes the generic loads."""
+    from w4a16 import int4_matmul, synth
+
+    say(f"gemm two K halves m={m} k={k} n={n}")
+    packed, scale = synth.make_weight(k, n, seed=k + n)
+    x = synth.make_activations(m, k, seed=m + k)
+    y = int4_matmul(x.to(DEV), packed.to(DEV), scale.to(DEV))
+    check_tolerance(y, orc.fused_reference(x.float().numpy(), packed.numpy(), scale.numpy()), f"M={m} K={k} N={n}")
+
+
 def test_unaligned_and_strided_activations():
     """Row stride > K, an activation pointer off 16-byte alignment (generic loads),
     and a transposed view (made contiguous by the wrapper)."""
