@@ -96,7 +96,8 @@ int w4a16_workspace_size(int M, int N, int K, int group_size, size_t* bytes);
  * group_size must be 128 (the reference asserts the same,
  * engine/kernels/quant.py:267).  K must be a multiple of 128.  M == 0 or
  * N == 0 is a no-op; K == 0 writes zeros.  M <= 32 runs the bandwidth-bound
- * decode kernels, M > 32 the MFMA GEMM.
+ * decode kernel, M > 64 the MFMA GEMM; 32 < M <= 64 takes the decode kernel
+ * when N/64 * K/1024 <= 1024 (its workgroup count), else the GEMM.
  */
 int w4a16_linear(const void* x, int64_t ldx,
                  const int8_t* packed, int64_t ldp,
@@ -109,8 +110,9 @@ int w4a16_linear(const void* x, int64_t ldx,
 /*
  * Several independent projections: up to W4A16_MAX_PROBLEMS problems, each
  * with its own M, activations, weights and output (problems may share x, e.g.
- * q/k/v or gate/up of a decoder block).  Problems with M <= 32 run in one
- * decode launch and problems with M > 32 in one GEMM launch.  Same arithmetic and status codes as
+ * q/k/v or gate/up of a decoder block).  Problems that take the decode
+ * kernel (see w4a16_linear) run in one decode launch, the rest in one GEMM
+ * launch.  Same arithmetic and status codes as
  * w4a16_linear; the workspace must be at least w4a16_workspace_size_grouped()
  * for the same table.
  *
@@ -133,7 +135,7 @@ int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int g
  *
  * Replaces `silu(linear(x, gate)) * linear(x, up)` of the reference MLP
  * (engine/llama_mlp.py:30-32, engine/llama_moe.py:44), i.e. two int4_matmul
- * launches plus two elementwise kernels.  M <= 32 runs one decode launch that
+ * launches plus two elementwise kernels.  Decode-sized M (as in w4a16_linear) runs one decode launch that
  * streams both weights and applies the epilogue to the fp32 sums (the
  * reference rounds gate and up to bf16 first; results agree to bf16 rounding).
  * Larger M computes gate into h and up into workspace, then one elementwise

@@ -10,9 +10,9 @@
 // A launch processes a table of up to kMaxProblems independent projections
 // that share M (one problem for the drop-in int4_matmul; q/k/v or gate/up or
 // a set of MoE experts for grouped calls).  Kernels:
-//   gemv_kernel     M <= 32  (decode, batched decode / verify)  HBM bound
+//   gemv_kernel     M <= 32, or <= 64 on small shapes (decode, batched decode)  HBM bound
 //   rowsum_kernel   per-(group,row) activation sums for gemm_kernel
-//   gemm_kernel     M > 32 (prefill)                        MFMA bound
+//   gemm_kernel     larger M (prefill)                      MFMA bound
 //   splitk_reduce_kernel  ordered sum of gemm_kernel's K-split partials
 //   zero_kernel     y = 0 for K == 0
 //   dequant_kernel  packed -> dense weights (bit-exactness probe of the unpack)
@@ -88,7 +88,7 @@ __device__ __forceinline__ int problem_of(const Launch& L, int wg) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-K reduction shared by the M <= 32 kernels, without atomics.
+// Split-K reduction of the decode kernel, without atomics.
 //
 // The workgroup of the last split (split == nsplit - 1) of a strip finishes
 // it; the others publish their fp32 partial and exit.  A published slot holds
@@ -229,8 +229,9 @@ __device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split
 }
 
 // ---------------------------------------------------------------------------
-// Decode GEMV kernel (M <= 32): the HBM-bound path of decode and of small
-// batches (M > 16 runs two 16-row M subtiles that share every unpacked weight).
+// Decode GEMV kernel (M <= 64): the HBM-bound path of decode and of small
+// batches (M > 16 runs two or four 16-row M subtiles that share every
+// unpacked weight).
 //
 // Lane mapping: a wave owns 16*CPL output columns;
 // lane l covers columns col0 = n0 + CPL*(l%16) .. +CPL and, inside each 32-row
@@ -497,7 +498,7 @@ __global__ __launch_bounds__(256) void rowsum_kernel(Launch L) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMM kernel (M > 32).
+// GEMM kernel (prefill-sized M).
 //
 // Workgroup tile 128 rows x 64*CPL columns, 4 waves side by side along N, each
 // wave 128 x 16*CPL (8 M-subtiles x CPL MFMA column blocks, CPL columns per
@@ -1122,20 +1123,28 @@ int check_problem(const w4a16_problem& q) {
 
 bool gemm_x_ok(const w4a16_problem& q) { return aligned(q.x, 16) && q.ldx % 8 == 0; }
 
-inline Kind kind_of(int M) {
-  static const int gemv_max = env_int("W4A16_GEMV_MAX", 32);
-  return M <= gemv_max ? kGemv : kGemm;
+// Kernel family of a problem.  M <= 32: decode kernel.  32 < M <= 64: the
+// decode kernel as well (four M subtiles, one 8-wave workgroup per CU) when it
+// launches at most 1024 workgroups, the GEMM otherwise (measured at M = 40
+// and 64: Qwen3-8B q/k 1.6-1.8x faster than the GEMM, gate/down within 10%,
+// Qwen3-32B gate/down 1.2-1.7x slower).
+inline Kind kind_of(const w4a16_problem& q) {
+  static const int gemv_max = env_int("W4A16_GEMV_MAX", 64);
+  if (q.M <= 32 && q.M <= gemv_max) return kGemv;
+  if (q.M > gemv_max) return kGemm;
+  const int64_t wgs = (int64_t)ceil_div(q.N, 64) * ceil_div(q.K / kGroup, 8);
+  return wgs <= 1024 ? kGemv : kGemm;
 }
 
 // Plan one launch over problems that all have M > 0, N > 0, K > 0 and the
-// same kind (kind_of(M)).
+// same kind (kind_of).
 Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
   Plan pl{};
   pl.pair = pair;
   pl.L.count = count;
   int max_m = 0;
   for (int i = 0; i < count; ++i) max_m = std::max(max_m, probs[i].M);
-  pl.kind = kind_of(max_m);
+  pl.kind = kind_of(probs[0]);
   bool full = true;
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = probs[i];
@@ -1335,12 +1344,12 @@ void launch_gemv_rows(const Plan& pl, dim3 grid, int max_m, hipStream_t s) {
     launch_gemv_as<CPL, WAVES, MULTI, 8, PAIR>(pl, grid, s);
   else if (max_m <= 16)
     launch_gemv_as<CPL, WAVES, MULTI, 16, PAIR>(pl, grid, s);
-#ifdef W4A16_EXP
-  else if (max_m > 32)
-    launch_gemv_as<CPL, WAVES, MULTI, 64, PAIR>(pl, grid, s);
-#endif
-  else
-    launch_gemv_as<CPL, WAVES, MULTI, 32, PAIR>(pl, grid, s);
+  else if constexpr (CPL == 4 && WAVES == 8) {  // the only shape make_plan picks for M > 16
+    if (max_m <= 32)
+      launch_gemv_as<CPL, WAVES, MULTI, 32, PAIR>(pl, grid, s);
+    else
+      launch_gemv_as<CPL, WAVES, MULTI, 64, PAIR>(pl, grid, s);
+  }
 }
 
 template <int CPL, int WAVES>
@@ -1387,7 +1396,7 @@ Batches split(const w4a16_problem* probs, int count) {
       b.sep[b.n_sep++] = q;
       continue;
     }
-    if (kind_of(q.M) == kGemv)
+    if (kind_of(q) == kGemv)
       b.gemv[b.n_gemv++] = q;
     else
       b.gemm[b.n_gemm++] = q;
@@ -1418,7 +1427,11 @@ int launch_plan(const w4a16_problem* probs, int count, void* workspace, size_t w
   if (need > 0 && (!workspace || workspace_bytes < need)) return W4A16_ERR_WORKSPACE;
   bind(pl, workspace, workspace_bytes);
   if (pl.kind == kGemv) {
-    if (pl.waves == 8) return pl.cpl == 4 ? launch_gemv<4, 8>(pl, s) : launch_gemv<8, 8>(pl, s);
+    if (pl.waves == 8 && pl.cpl == 4) return launch_gemv<4, 8>(pl, s);
+    int max_m = 0;
+    for (int i = 0; i < count; ++i) max_m = std::max(max_m, probs[i].M);
+    if (max_m > 16) return W4A16_ERR_LAUNCH;  // no kernel built for that shape
+    if (pl.waves == 8) return launch_gemv<8, 8>(pl, s);
     return pl.cpl == 4 ? launch_gemv<4, 4>(pl, s) : launch_gemv<8, 4>(pl, s);
   }
   hipLaunchKernelGGL(rowsum_kernel, dim3(pl.rs_wgs), dim3(256), 0, s, pl.L);
@@ -1484,7 +1497,7 @@ int workspace_for(const w4a16_problem* probs, int count, size_t* bytes, size_t s
 // one decode launch whose finishers apply the epilogue to the fp32 sums.
 // Larger M: gate into h and up into the first `ubytes` of the upper workspace
 // half (one grouped launch), then silu_mul_kernel.
-size_t swiglu_up_bytes(int M, int N) { return kind_of(M) == kGemv ? 0 : align256((size_t)M * N * 2); }
+size_t swiglu_up_bytes(const w4a16_problem& q) { return kind_of(q) == kGemv ? 0 : align256((size_t)q.M * q.N * 2); }
 
 int swiglu(const w4a16_problem pair[2], void* workspace, size_t workspace_bytes, hipStream_t s) {
   const w4a16_problem& g = pair[0];
@@ -1494,8 +1507,8 @@ int swiglu(const w4a16_problem pair[2], void* workspace, size_t workspace_bytes,
                        static_cast<uint16_t*>(g.y), g.ldy, g.M, g.N);
     return launch_status();
   }
-  if (kind_of(g.M) == kGemv) return launch_plan(pair, 2, workspace, workspace_bytes, s, 0, true);
-  const size_t ub = swiglu_up_bytes(g.M, g.N);
+  if (kind_of(g) == kGemv) return launch_plan(pair, 2, workspace, workspace_bytes, s, 0, true);
+  const size_t ub = swiglu_up_bytes(g);
   if (!workspace || workspace_bytes < 2 * ub + 256) return W4A16_ERR_WORKSPACE;
   w4a16_problem q[2] = {pair[0], pair[1]};
   uint16_t* u = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + ((workspace_bytes / 2) & ~(size_t)255));
@@ -1512,8 +1525,8 @@ int swiglu_workspace(const w4a16_problem pair[2], size_t* bytes) {
   *bytes = 0;
   const w4a16_problem& g = pair[0];
   if (g.M == 0 || g.N == 0 || g.K == 0) return W4A16_OK;
-  if (kind_of(g.M) == kGemv) return plan_workspace(pair, 2, bytes, 0, true);
-  const size_t ub = swiglu_up_bytes(g.M, g.N);
+  if (kind_of(g) == kGemv) return plan_workspace(pair, 2, bytes, 0, true);
+  const size_t ub = swiglu_up_bytes(g);
   const int rc = workspace_for(pair, 2, bytes, ub);
   *bytes = std::max(*bytes, 2 * ub + 256);
   return rc;

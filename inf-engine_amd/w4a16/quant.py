@@ -127,8 +127,8 @@ def int4_matmul_grouped(a, weights, group_size: int = 128) -> list[torch.Tensor]
     ``a`` is one ``(M, K)`` bf16 tensor shared by every projection (q/k/v or
     gate/up of a block) or a list of per-projection activations, each with its
     own M (a set of MoE experts with their token counts).  ``weights`` is a list
-    of ``(packed, scale)`` pairs, at most 16.  Projections with M <= 32 share one
-    decode launch and those with M > 32 one GEMM launch.  Results equal
+    of ``(packed, scale)`` pairs, at most 16.  Decode-sized projections (M <= 32,
+    or M <= 64 on small shapes) share one decode launch and the rest one GEMM launch.  Results equal
     ``int4_matmul`` on each pair up to fp32 summation order.  No reference
     counterpart: the reference calls ``int4_matmul`` once per projection
     (engine/llama_attention.py:83-85, engine/llama_mlp.py:30-33,
@@ -151,7 +151,8 @@ def int4_matmul(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, grou
     enqueues on the current stream and never synchronises, so it can be
     captured in a HIP graph once its workspace exists.
 
-    M <= 32 runs the HBM-bound decode kernels, larger M the MFMA GEMM.
+    M <= 32 (M <= 64 on small shapes) runs the HBM-bound decode kernel, larger M
+    the MFMA GEMM.
 
     Raises:
         AssertionError: ``group_size != 128`` (as engine/kernels/quant.py:267).
@@ -169,7 +170,7 @@ def int4_swiglu(a: torch.Tensor, gate, up, group_size: int = 128) -> torch.Tenso
     ``gate`` and ``up`` are ``(packed, scale)`` pairs of the same shape.  The
     reference computes ``silu(linear(x, gate)) * linear(x, up)``
     (engine/llama_mlp.py:30-32, engine/llama_moe.py:44) as two int4_matmul
-    launches and two elementwise kernels; here M <= 32 is a single decode
+    launches and two elementwise kernels; here decode-sized M is a single decode
     launch with the epilogue on the fp32 sums, larger M the grouped GEMM plus
     one elementwise pass.  Same checks and exceptions as ``int4_matmul``.
     """
