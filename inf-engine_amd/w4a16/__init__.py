@@ -10,7 +10,7 @@ in hand-written gfx950 HIP kernels behind the C ABI of include/w4a16.h.
 
 from .checkpoint import load_int4, load_quantized_llama, save_int4
 from . import moe
-from .layers import linear, lm_head, swiglu_mlp
+from .layers import linear, lm_head, qkv_projections, swiglu_mlp
 from .quant import (
     dequantize_weight_int4,
     int4_matmul,
@@ -24,6 +24,7 @@ __all__ = [
     "linear",
     "lm_head",
     "swiglu_mlp",
+    "qkv_projections",
     "int4_swiglu",
     "int4_matmul",
     "int4_matmul_grouped",

@@ -43,6 +43,25 @@ def swiglu_mlp(x: torch.Tensor, weights: dict) -> torch.Tensor:
     return linear(h.reshape(*lead, g.shape[0]), d)
 
 
+def qkv_projections(x: torch.Tensor, weights: dict) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``q, k, v = linear(x, W_q), linear(x, W_k), linear(x, W_v)`` (engine/llama_attention.py:83-85).
+
+    With INT4 weights (group size 128) on a HIP device the three projections
+    share one grouped launch (``int4_matmul_grouped``); otherwise three
+    ``linear`` calls as in the reference.  Shapes as the reference:
+    ``x (..., d_model)`` -> ``(..., d_out)`` each.
+    """
+    from .quant import int4_matmul_grouped
+
+    ws = [weights[f"self_attn.{n}_proj.weight"] for n in ("q", "k", "v")]
+    fused = all(hasattr(w, "packed") and getattr(w, "group_size", None) == 128 for w in ws) and x.is_cuda
+    if not fused:
+        return tuple(linear(x, w) for w in ws)
+    lead = x.shape[:-1]
+    outs = int4_matmul_grouped(x.reshape(-1, x.shape[-1]), [(w.packed, w.scale) for w in ws], 128)
+    return tuple(o.reshape(*lead, w.shape[0]) for o, w in zip(outs, ws))
+
+
 def lm_head(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """Logits ``x @ weight.T`` for a dense bf16 ``weight[vocab, d_model]`` (engine/llama_model.py:148).
 

@@ -641,3 +641,28 @@ def test_swiglu_mlp_layer_matches_unfused():
         err = float((out.double() - ref).abs().max())
         say(f"  swiglu_mlp m={m}: max|d|/rms={err / rms:.3e}")
         assert err <= 2e-2 * rms
+
+
+def test_qkv_projections_grouped_matches_linear():
+    """qkv_projections (one grouped launch) equals three linear() calls; decode
+    sizes bit for bit (same decode arithmetic), prefill sizes to the bar."""
+    from w4a16 import _Int4Weight, linear, qkv_projections, synth
+
+    d, nq, nkv = 512, 512, 128
+    ws = {}
+    for name, n, seed in (("q", nq, 1), ("k", nkv, 2), ("v", nkv, 3)):
+        p, s = synth.make_weight(d, n, seed=700 + seed, device=DEV)
+        ws[f"self_attn.{name}_proj.weight"] = _Int4Weight(p, s, 128, (n, d))
+    for m in (1, 3, 96):
+        x = synth.make_activations(2 * m, d, seed=710 + m, device=DEV).reshape(2, m, d)
+        q, k, v = qkv_projections(x, ws)
+        for out, name, n in ((q, "q", nq), (k, "k", nkv), (v, "v", nkv)):
+            assert out.shape == (2, m, n)
+            ref = linear(x, ws[f"self_attn.{name}_proj.weight"])
+            if m <= 16:
+                assert torch.equal(out, ref), (name, m)
+            else:
+                w = ws[f"self_attn.{name}_proj.weight"]
+                y64 = orc.fused_reference(x.reshape(-1, d).float().cpu().numpy(), w.packed.cpu().numpy(),
+                                          w.scale.cpu().numpy())
+                check_tolerance(out.reshape(-1, n), y64, f"qkv {name} M={2 * m}")
