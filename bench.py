@@ -181,7 +181,7 @@ def roofline_decode(us: float) -> dict:
         "unit": "GB/s",
         "frac": round(ach / HBM_PEAK_GBS, 4),
         "traffic": read_traffic(TRAFFIC_FILE),
-        "kernel": "gemv_kernel<8, 4, true, false, 1> (gate_proj K=4096 N=12288 M=1, one launch of int4_matmul)",
+        "kernel": "gemv_kernel<8, 4, true, false, 1, false> (gate_proj K=4096 N=12288 M=1, one launch of int4_matmul)",
         "bytes_per_launch": b,
         "avg_launch_us": round(us, 3),
     }
@@ -199,7 +199,7 @@ def roofline_prefill(us: float) -> dict:
         "unit": "TFLOP/s",
         "frac": round(ach / BF16_PEAK_TFLOPS, 4),
         "traffic": read_traffic(TRAFFIC_FILE_PREFILL),
-        "kernel": "gemm_kernel<4, true> (gate_proj K=4096 N=12288 M=2048), after rowsum_kernel",
+        "kernel": "gemm_kernel<4, true, 1> (gate_proj K=4096 N=12288 M=2048), after rowsum_kernel",
         "flops_per_launch": f,
         "avg_launch_us": round(us, 3),
     }
