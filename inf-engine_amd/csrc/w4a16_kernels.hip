@@ -115,14 +115,23 @@ __device__ __forceinline__ uint32_t publish_bits(float v) {
   return ~b;
 }
 
-// Poll-and-sum of nslots published slots (stride elements apart) for a
-// thread's EPT elements.  All of a thread's polls for a chunk of SCH slots are
-// in flight at once, so a thread with several elements waits about one round
-// trip per chunk rather than one per element.  Sums in slot order into v;
-// zeroes what it read.
+// Poll-and-sum of nslots published slots (stride bytes apart) for a
+// thread's EPT elements at byte offsets off[].  All of a thread's polls for a
+// chunk of SCH slots are in flight at once, so a thread with several elements
+// waits about one round trip per chunk rather than one per element.  Sums in
+// slot order into v; zeroes what it read.
+//
+// The code is kept short and branch-free outside the spin loop: only the
+// finishing workgroup runs it, so its instructions are not in the CU's
+// instruction cache and every one of them is fetched on the critical path
+// of the launch (MI355X: 512 added instructions there cost 0.25-0.8 us per
+// launch).  Polls are unconditional buffer loads; slots past nslots lie
+// beyond the resource's range and read 0 without touching memory, and are
+// masked out.
 template <int EPT>
-__device__ __forceinline__ void sum_slots(uint32_t* slots, int nslots, size_t stride, const size_t (&off)[EPT],
-                                          const bool (&ok)[EPT], float (&v)[EPT], bool& timed_out) {
+__device__ __forceinline__ void sum_slots(__amdgpu_buffer_rsrc_t rs, int nslots, uint32_t stride,
+                                          const uint32_t (&off)[EPT], const bool (&ok)[EPT], float (&v)[EPT],
+                                          bool& timed_out) {
   constexpr int SCH = EPT >= 8 ? 2 : (EPT >= 4 ? 4 : 8);  // slots per chunk: EPT * SCH polls in flight
   for (int sp0 = 0; sp0 < nslots; sp0 += SCH) {
     uint32_t t[EPT][SCH];
@@ -130,39 +139,42 @@ __device__ __forceinline__ void sum_slots(uint32_t* slots, int nslots, size_t st
     for (int j = 0; j < EPT; ++j)
 #pragma unroll
       for (int i = 0; i < SCH; ++i)
-        t[j][i] = ok[j] && sp0 + i < nslots ? __hip_atomic_load(slots + (size_t)(sp0 + i) * stride + off[j],
-                                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                            : 1u;
+        t[j][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, off[j] + (uint32_t)(sp0 + i) * stride, 0, kAgentCoherent);
+    // A slot is still empty when it reads 0, lies within nslots and belongs to one of our elements.
+    auto empty = [&](int j, int i) { return t[j][i] == 0u && sp0 + i < nslots && ok[j]; };
+    // Wave-uniform loop: every round re-polls all SCH slots and keeps the
+    // ones that had already arrived.
     for (uint32_t spins = 0;; ++spins) {
       bool missing = false;
 #pragma unroll
       for (int j = 0; j < EPT; ++j)
 #pragma unroll
-        for (int i = 0; i < SCH; ++i) missing = missing || t[j][i] == 0u;
-      if (!missing) break;
+        for (int i = 0; i < SCH; ++i) missing = missing | empty(j, i);  // bitwise: no short-circuit branches
+      if (__builtin_amdgcn_ballot_w64(missing) == 0) break;
       if (spins == kSpinLimit) {
         timed_out = true;
         break;
       }
+      asm volatile("" ::: "memory");  // every round reloads from memory
 #pragma unroll
       for (int j = 0; j < EPT; ++j)
 #pragma unroll
-        for (int i = 0; i < SCH; ++i)
-          if (t[j][i] == 0u)
-            t[j][i] = __hip_atomic_load(slots + (size_t)(sp0 + i) * stride + off[j], __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
+        for (int i = 0; i < SCH; ++i) {
+          const uint32_t r =
+              __builtin_amdgcn_raw_buffer_load_b32(rs, off[j] + (uint32_t)(sp0 + i) * stride, 0, kAgentCoherent);
+          const uint32_t keep = t[j][i] != 0u ? ~0u : 0u;  // a mask, not a select, so the load stays unconditional
+          t[j][i] = (t[j][i] & keep) | (r & ~keep);
+        }
     }
 #pragma unroll
     for (int j = 0; j < EPT; ++j)
 #pragma unroll
-      for (int i = 0; i < SCH; ++i)
-        if (sp0 + i < nslots) v[j] += __uint_as_float(~t[j][i]);
+      for (int i = 0; i < SCH; ++i) v[j] += sp0 + i < nslots ? __uint_as_float(~t[j][i]) : 0.f;
   }
 #pragma unroll
   for (int j = 0; j < EPT; ++j)
-    if (ok[j])
-      for (int sp = 0; sp < nslots; ++sp)
-        __hip_atomic_store(slots + (size_t)sp * stride + off[j], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int sp = 0; sp < nslots; ++sp)
+      if (ok[j]) __builtin_amdgcn_raw_buffer_store_b32(0u, rs, off[j] + (uint32_t)sp * stride, 0, kAgentCoherent);
 }
 
 // x * sigmoid(x) in fp32 (engine/layers.py:28-30).
@@ -182,19 +194,22 @@ __device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split
                                               PartialFn partial, const Problem* gate = nullptr) {
   const int N = P.N;
   const int elems = rows * wcols;
-  const size_t stride = (size_t)M * N;
-  uint32_t* slots = reinterpret_cast<uint32_t*>(P.part);
+  // Slots are [nslots][M][N] fp32; byte offsets fit in 32 bits (make_plan).
+  const uint32_t stride = (uint32_t)M * (uint32_t)N * 4u;
   const int last = P.nsplit - 1;
+  const int nslots = MODE == kFinishGate ? P.nsplit : last;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(P.part, stride * (uint32_t)nslots);
   if (MODE == kFinishGate || split != last) {
-    uint32_t* dst = slots + (size_t)split * stride;
+    const uint32_t dst = (uint32_t)split * stride;
     for (int e = threadIdx.x; e < elems; e += NT) {
       const int m = e / wcols, c = e % wcols, n = n0 + c;
-      if (n < N) __hip_atomic_store(dst + (size_t)m * N + n, publish_bits(partial(e)), __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
+      if (n < N)
+        __builtin_amdgcn_raw_buffer_store_b32(publish_bits(partial(e)), rs, dst + ((uint32_t)m * N + n) * 4u, 0,
+                                              kAgentCoherent);
     }
     return;
   }
-  size_t off[EPT];
+  uint32_t off[EPT];
   bool ok[EPT];
   float own[EPT], v[EPT];
 #pragma unroll
@@ -202,17 +217,18 @@ __device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split
     const int e = threadIdx.x + j * NT;
     const int m = e / wcols, c = e % wcols, n = n0 + c;
     ok[j] = e < elems && n < N;
-    off[j] = ok[j] ? (size_t)m * N + n : 0;
+    off[j] = ok[j] ? ((uint32_t)m * N + n) * 4u : 0u;
     own[j] = ok[j] ? partial(e) : 0.f;
     v[j] = 0.f;
   }
   bool timed_out = false;
-  sum_slots<EPT>(slots, last, stride, off, ok, v, timed_out);
+  sum_slots<EPT>(rs, last, stride, off, ok, v, timed_out);
   if constexpr (MODE == kFinishUp) {
     float gv[EPT];
 #pragma unroll
     for (int j = 0; j < EPT; ++j) gv[j] = 0.f;
-    sum_slots<EPT>(reinterpret_cast<uint32_t*>(gate->part), gate->nsplit, stride, off, ok, gv, timed_out);
+    const __amdgpu_buffer_rsrc_t grs = make_rsrc(gate->part, stride * (uint32_t)gate->nsplit);
+    sum_slots<EPT>(grs, gate->nsplit, stride, off, ok, gv, timed_out);
 #pragma unroll
     for (int j = 0; j < EPT; ++j) v[j] = silu(gv[j]) * (v[j] + own[j]);
   } else {
@@ -1102,6 +1118,7 @@ struct Plan {
   size_t skip;         // bytes at the start of the upper workspace half reserved by the caller
   size_t lds_bytes;    // dynamic LDS (gemv)
   size_t ws_bytes;     // bytes of the plan's workspace half (see bind())
+  bool too_large;      // gemv: a problem's split-K slots exceed the finish's 32-bit byte offsets
   int total_wgs;
   int rs_wgs;          // rowsum_kernel workgroups
   int red_wgs;         // splitk_reduce_kernel workgroups (gemm with split K)
@@ -1217,6 +1234,7 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
       if (nslots > 0) {
         pl.part_off[i] = ws;
         ws = align256(ws + (size_t)nslots * M * P.N * 4);
+        if ((size_t)P.nsplit * M * P.N * 4 >= 0xffffffffull) pl.too_large = true;
       }
     }
     pl.lds_bytes = lds;
@@ -1426,6 +1444,7 @@ int launch_plan(const w4a16_problem* probs, int count, void* workspace, size_t w
   const size_t need = plan_bytes(pl);
   if (need > 0 && (!workspace || workspace_bytes < need)) return W4A16_ERR_WORKSPACE;
   bind(pl, workspace, workspace_bytes);
+  if (pl.too_large) return W4A16_ERR_TOO_LARGE;
   if (pl.kind == kGemv) {
     if (pl.waves == 8 && pl.cpl == 4) return launch_gemv<4, 8>(pl, s);
     int max_m = 0;
