@@ -321,8 +321,8 @@ __device__ __forceinline__ void decode_group(const DecodeSlot<CPL>& d, const bf1
 // One wave's share of a decode launch: the 128-row group g of problem P for
 // the lane's CPL columns starting at col0, accumulated into total.  Activation
 // fragments: lane (lc, lk) holds x[lc, g*128 + 32*st + 8*lk .. +8].  FULL
-// launches load them unconditionally (lanes past M read row 0) and zero them
-// with a select, so no branch or wait sits before the weight loads.
+// launches load them unconditionally (lanes past M read zeros from outside the
+// buffer's range), so no branch or wait sits before the weight loads.
 template <int CPL, bool FULL, int MT>
 __device__ __forceinline__ void decode_wave(const Problem& P, int g, int col0, int lc, int lk, int M,
                                             f32x4_t (&total)[MT][CPL]) {
@@ -335,14 +335,16 @@ __device__ __forceinline__ void decode_wave(const Problem& P, int g, int col0, i
     const int row = lc + 16 * mt;
     const uint32_t keep = row < M ? 0xffffffffu : 0u;
     if constexpr (FULL) {
+      // Lanes of rows past M get an offset beyond the resource's range (x is
+      // under 2 GB on this path, make_plan): their loads return zeros without
+      // a memory access, so at M = 1 only 4 lanes of 64 fetch activations.
       const __amdgpu_buffer_rsrc_t xrs = make_rsrc(P.x, (uint32_t)((size_t)P.ldx * 2 * M));
-      const uint32_t xoff = ((uint32_t)(row < M ? row : 0) * (uint32_t)P.ldx + (uint32_t)(g * kGroup + lk * 8)) * 2u;
+      const uint32_t xoff =
+          row < M ? ((uint32_t)row * (uint32_t)P.ldx + (uint32_t)(g * kGroup + lk * 8)) * 2u : 0x80000000u;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const u32x4_t v =
-            __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + st * 64, 0, 0));
-        A[mt][st] = as_bf16x8(v & keep);
-      }
+      for (int st = 0; st < 4; ++st)
+        A[mt][st] = as_bf16x8(
+            __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + st * 64, 0, 0)));
     } else {
       const bool vec_x = (P.vec & 2) != 0;
       const uint16_t* xrow = P.x + (int64_t)(row < M ? row : 0) * P.ldx + (int64_t)g * kGroup + lk * 8;
@@ -1227,7 +1229,7 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
       const size_t wbytes = (size_t)(P.K / 2) * P.ldp, sbytes = (size_t)G * P.lds * 4;
       const size_t xbytes = (size_t)P.ldx * 2 * M;
       full = full && (P.vec & 1) && (P.vec & 2) && P.N % wcols == 0 && wbytes < 0xffffffffull &&
-             sbytes < 0xffffffffull && xbytes < 0xffffffffull;
+             sbytes < 0xffffffffull && xbytes < 0x80000000ull;  // x: rows past M read at offset 2^31
       // Published slots: nsplit - 1 per strip (the last split finishes), all
       // nsplit for the gate of a pair (up's finisher reads them).
       const int nslots = pair && i == 0 ? P.nsplit : P.nsplit - 1;
