@@ -39,7 +39,8 @@ extern "C" {
 #define W4A16_ERR_WORKSPACE 5   /* workspace NULL or smaller than w4a16_workspace_size() */
 #define W4A16_ERR_LAUNCH 6      /* a HIP launch reported an error */
 #define W4A16_ERR_DTYPE 7       /* unknown dtype code */
-#define W4A16_ERR_TOO_LARGE 8   /* problem exceeds what the entry point supports (w4a16_bf16_gemv: M > 16) */
+#define W4A16_ERR_TOO_LARGE 8   /* problem exceeds what the entry point supports (w4a16_bf16_gemv: M > 16;
+                                   decode-sized M whose split-K partials, nsplit * M * N * 4 bytes, reach 4 GB) */
 
 /* dtype codes for w4a16_dequant. */
 #define W4A16_DTYPE_F32 0

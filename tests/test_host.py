@@ -60,6 +60,19 @@ def test_linear_argument_validation_returns_codes(native_lib):
     assert _linear(lib, n=0, x=None, packed=None, scale=None, y=None) == nat.W4A16_OK
 
 
+def test_linear_rejects_split_k_slots_past_32_bit_offsets(native_lib):
+    """Decode shapes whose published split-K slots exceed 4 GB are refused before any launch
+    (the finish addresses slots with 32-bit byte offsets); no pointer is dereferenced."""
+    from w4a16 import _native as nat
+
+    m, n, k = 32, 1 << 20, 128 * 1024  # 128 K splits x 32 rows x 2^20 columns of fp32 = 16 GB of slots
+    need = ctypes.c_size_t(0)
+    assert native_lib.w4a16_workspace_size(m, n, k, 128, ctypes.byref(need)) == nat.W4A16_OK
+    assert need.value > 1 << 32
+    rc = _linear(native_lib, ldx=k, ldp=n, lds=n, ldy=n, m=m, n=n, k=k, ws=4096, ws_bytes=need.value)
+    assert rc == nat.W4A16_ERR_TOO_LARGE
+
+
 def test_grouped_argument_validation(native_lib):
     from w4a16 import _native as nat
 
