@@ -124,6 +124,21 @@ def check(code: int, what: str) -> None:
     raise RuntimeError(msg)
 
 
+def _rows(t: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """``t`` as rows the C ABI can address, and its row stride in elements.
+
+    The kernels read unit-stride rows ``ld`` elements apart.  Views whose
+    columns are strided, or whose rows overlap (row stride below the row width,
+    e.g. ``x.expand(M, K)``), are copied; a single row may have any row stride,
+    since only that row is read.  The reference's Triton kernel honours such
+    strides (engine/kernels/quant.py:275), so they are accepted here too.
+    """
+    rows, width = t.shape
+    if t.stride(1) != 1 or (rows > 1 and t.stride(0) < width):
+        t = t.contiguous()
+    return t, (t.stride(0) if rows > 1 else max(t.stride(0), width))
+
+
 def workspace_size(m: int, n: int, k: int, group_size: int = 128) -> int:
     out = ctypes.c_size_t(0)
     check(load_library().w4a16_workspace_size(m, n, k, group_size, ctypes.byref(out)), "w4a16_workspace_size")
@@ -163,20 +178,17 @@ def linear(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_siz
     lib = load_library()
     m, k = a.shape
     n = packed.shape[1]
-    if a.stride(1) != 1:
-        a = a.contiguous()
-    if packed.stride(1) != 1:
-        packed = packed.contiguous()
-    if scale.stride(1) != 1:
-        scale = scale.contiguous()
+    a, ldx = _rows(a)
+    packed, ldp = _rows(packed)
+    scale, lds = _rows(scale)
     y = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
     stream = torch.cuda.current_stream(a.device).cuda_stream
     nbytes = workspace_size(m, n, k, group_size)
     ws = get_workspace(a.device, stream, nbytes)
     rc = lib.w4a16_linear(
-        a.data_ptr(), a.stride(0),
-        packed.data_ptr(), packed.stride(0),
-        scale.data_ptr(), scale.stride(0),
+        a.data_ptr(), ldx,
+        packed.data_ptr(), ldp,
+        scale.data_ptr(), lds,
         y.data_ptr(), y.stride(0),
         m, n, k, group_size,
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
@@ -194,18 +206,15 @@ def linear_grouped(xs, weights, group_size: int) -> list[torch.Tensor]:
     table = (Problem * len(weights))()
     outs, keep = [], []
     for i, (x, (packed, scale)) in enumerate(zip(xs, weights)):
-        if x.stride(1) != 1:
-            x = x.contiguous()
-        if packed.stride(1) != 1:
-            packed = packed.contiguous()
-        if scale.stride(1) != 1:
-            scale = scale.contiguous()
+        x, ldx = _rows(x)
+        packed, ldp = _rows(packed)
+        scale, lds = _rows(scale)
         keep += [x, packed, scale]
         m, n = x.shape[0], packed.shape[1]
         y = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
         outs.append(y)
-        table[i] = Problem(x.data_ptr(), x.stride(0), packed.data_ptr(), packed.stride(0), scale.data_ptr(),
-                           scale.stride(0), y.data_ptr(), y.stride(0), m, n, x.shape[1])
+        table[i] = Problem(x.data_ptr(), ldx, packed.data_ptr(), ldp, scale.data_ptr(), lds,
+                           y.data_ptr(), y.stride(0), m, n, x.shape[1])
     dev = xs[0].device
     stream = torch.cuda.current_stream(dev).cuda_stream
     nbytes = ctypes.c_size_t(0)
@@ -223,12 +232,13 @@ def swiglu(a: torch.Tensor, gate, up, group_size: int) -> torch.Tensor:
     """h = silu(a @ Wg) * (a @ Wu) on the current HIP stream; gate/up are (packed, fp32 scale)."""
     lib = load_library()
     m, k = a.shape
-    if a.stride(1) != 1:
-        a = a.contiguous()
-    ops = []
+    a, ldx = _rows(a)
+    ops, lds_ = [], []
     for packed, scale in (gate, up):
-        ops += [packed if packed.stride(1) == 1 else packed.contiguous(),
-                scale if scale.stride(1) == 1 else scale.contiguous()]
+        for t in (packed, scale):
+            t, ld = _rows(t)
+            ops.append(t)
+            lds_.append(ld)
     n = ops[0].shape[1]
     h = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
     stream = torch.cuda.current_stream(a.device).cuda_stream
@@ -236,9 +246,9 @@ def swiglu(a: torch.Tensor, gate, up, group_size: int) -> torch.Tensor:
     check(lib.w4a16_workspace_size_swiglu(m, n, k, group_size, ctypes.byref(nbytes)), "w4a16_workspace_size_swiglu")
     ws = get_workspace(a.device, stream, nbytes.value)
     rc = lib.w4a16_swiglu(
-        a.data_ptr(), a.stride(0),
-        ops[0].data_ptr(), ops[0].stride(0), ops[1].data_ptr(), ops[1].stride(0),
-        ops[2].data_ptr(), ops[2].stride(0), ops[3].data_ptr(), ops[3].stride(0),
+        a.data_ptr(), ldx,
+        ops[0].data_ptr(), lds_[0], ops[1].data_ptr(), lds_[1],
+        ops[2].data_ptr(), lds_[2], ops[3].data_ptr(), lds_[3],
         h.data_ptr(), h.stride(0),
         m, n, k, group_size,
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
@@ -253,13 +263,11 @@ def bf16_gemv(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     lib = load_library()
     m, k = x.shape
     n = w.shape[0]
-    if x.stride(1) != 1:
-        x = x.contiguous()
-    if w.stride(1) != 1:
-        w = w.contiguous()
+    x, ldx = _rows(x)
+    w, ldw = _rows(w)
     y = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
     stream = torch.cuda.current_stream(x.device).cuda_stream
-    rc = lib.w4a16_bf16_gemv(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(), y.stride(0),
+    rc = lib.w4a16_bf16_gemv(x.data_ptr(), ldx, w.data_ptr(), ldw, y.data_ptr(), y.stride(0),
                              m, n, k, stream)
     check(rc, "w4a16_bf16_gemv")
     return y
@@ -274,16 +282,14 @@ def dequant(packed: torch.Tensor, scale: torch.Tensor, group_size: int, out_dtyp
         code = DTYPE_BF16
     else:
         raise TypeError(f"w4a16 dequant supports float32 and bfloat16 outputs, got {out_dtype}")
-    if packed.stride(1) != 1:
-        packed = packed.contiguous()
-    if scale.stride(1) != 1:
-        scale = scale.contiguous()
+    packed, ldp = _rows(packed)
+    scale, lds = _rows(scale)
     k = packed.shape[0] * 2
     n = packed.shape[1]
     out = torch.empty((k, n), device=packed.device, dtype=out_dtype)
     stream = torch.cuda.current_stream(packed.device).cuda_stream
     rc = lib.w4a16_dequant(
-        packed.data_ptr(), packed.stride(0), scale.data_ptr(), scale.stride(0),
+        packed.data_ptr(), ldp, scale.data_ptr(), lds,
         out.data_ptr(), out.stride(0), code, k, n, group_size, stream,
     )
     check(rc, "w4a16_dequant")

@@ -198,6 +198,35 @@ def test_unaligned_and_strided_activations():
         check_tolerance(int4_matmul(xt, packed, scale), y_ref, f"transposed M={m}")
 
 
+def test_overlapping_rows_and_single_row_strides():
+    """Views the reference's stride-honouring Triton kernel accepts
+    (engine/kernels/quant.py:275): rows that overlap (x.expand, row stride 0),
+    a single row whose row stride is below K, and strided weight views."""
+    from w4a16 import int4_matmul, int4_matmul_grouped
+
+    for m in (1, 5, 64):
+        say(f"expanded rows m={m}")
+        x1, packed, scale = rand_problem(1, 512, 256, seed=40 + m)
+        xe = x1[0].expand(m, 512)
+        assert m == 1 or xe.stride() == (0, 1)  # torch keeps stride K on a size-1 dim
+        y_ref = np.repeat(orc.fused_reference(x1.float().cpu().numpy(), packed.cpu().numpy(),
+                                              scale.cpu().numpy()), m, axis=0)
+        check_tolerance(int4_matmul(xe, packed, scale), y_ref, f"expand M={m}")
+        (yg,) = int4_matmul_grouped(xe, [(packed, scale)])
+        check_tolerance(yg, y_ref, f"expand grouped M={m}")
+    say("single row, row stride 1")
+    x1, packed, scale = rand_problem(1, 512, 256, seed=50)
+    xs = x1.as_strided((1, 512), (1, 1))
+    y_ref = orc.fused_reference(x1.float().cpu().numpy(), packed.cpu().numpy(), scale.cpu().numpy())
+    check_tolerance(int4_matmul(xs, packed, scale), y_ref, "single row stride 1")
+    say("column-major weights")
+    x, packed, scale = rand_problem(3, 512, 256, seed=51)
+    y_ref = orc.fused_reference(x.float().cpu().numpy(), packed.cpu().numpy(), scale.cpu().numpy())
+    pt = packed.t().contiguous().t()
+    st = scale.t().contiguous().t()
+    check_tolerance(int4_matmul(x, pt, st), y_ref, "column-major packed/scale")
+
+
 def test_empty_and_zero_k():
     from w4a16 import int4_matmul
 
