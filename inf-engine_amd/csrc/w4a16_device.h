@@ -49,6 +49,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
+// Two fp32 values -> a packed bf16 pair (a in the low half), round to nearest
+// even, through gfx950's packed conversion (one VALU op).  Finite values and
+// infinities round exactly as f32_to_bf16; a NaN stays a quiet NaN but keeps
+// its sign and leading payload bits instead of becoming 0x7FC0.
+typedef float f32x2v_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v_t{a, b}, bf16x2_t));
+}
+
 // 16x16x32 bf16 MFMA.  Operand layout (lane l): A[m = l%16][k = 8*(l/16) + j],
 // B[k = 8*(l/16) + j][n = l%16] for j = 0..7; D[m = 4*(l/16) + r][n = l%16].
 __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {

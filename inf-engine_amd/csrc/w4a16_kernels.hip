@@ -861,19 +861,19 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
         const int m = m0 + 16 * i + 4 * lk + r;
         if (m >= M) continue;
         uint16_t* dst = P.y + (int64_t)m * P.ldy + col0;
-        uint16_t h[CPL];
+        // Column pairs through the hardware packed conversion (one VALU op per two outputs).
+        uint32_t h2[CPL / 2];
 #pragma unroll
-        for (int t = 0; t < CPL; ++t) h[t] = f32_to_bf16(U[i][t][r] * s_ref[t]);
+        for (int t = 0; t < CPL; t += 2) h2[t / 2] = bf16x2_rne(U[i][t][r] * s_ref[t], U[i][t + 1][r] * s_ref[t + 1]);
         if (vec_y) {
           if constexpr (CPL == 4)
-            *reinterpret_cast<u32x2_t*>(dst) =
-                u32x2_t{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{h2[0], h2[1]};
           else
-            *reinterpret_cast<uint32_t*>(dst) = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+            *reinterpret_cast<uint32_t*>(dst) = h2[0];
         } else {
 #pragma unroll
           for (int t = 0; t < CPL; ++t)
-            if (col0 + t < N) dst[t] = h[t];
+            if (col0 + t < N) dst[t] = (uint16_t)(h2[t / 2] >> (16 * (t & 1)));
         }
       }
     return;
