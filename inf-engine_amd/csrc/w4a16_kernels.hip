@@ -852,6 +852,29 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
   }
 
   // ---- output: lane holds rows m0 + 16i + 4lk + r, columns col0 .. col0+CPL-1 ----
+  if (P.nsplit == 1 && FULL && m0 + kGemmRows <= M && (P.vec & 4) != 0 &&
+      (size_t)kGemmRows * P.ldy * 2 < 0xffffffffull) {
+    // Whole tile in range: buffer stores off a resource at the tile's first
+    // row, the lane's column offset in a VGPR and the row offset as a scalar,
+    // so the stores need no per-row address arithmetic or bounds checks.
+    const uint32_t ldy2 = (uint32_t)P.ldy * 2u;
+    const __amdgpu_buffer_rsrc_t yrs = make_rsrc(P.y + (int64_t)m0 * P.ldy, kGemmRows * ldy2);
+    const uint32_t yv = (uint32_t)(4 * lk) * ldy2 + (uint32_t)col0 * 2u;
+#pragma unroll
+    for (int i = 0; i < kGemmMT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        uint32_t h2[CPL / 2];
+#pragma unroll
+        for (int t = 0; t < CPL; t += 2) h2[t / 2] = bf16x2_rne(U[i][t][r] * s_ref[t], U[i][t + 1][r] * s_ref[t + 1]);
+        const uint32_t so = (uint32_t)(16 * i + r) * ldy2;
+        if constexpr (CPL == 4)
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{h2[0], h2[1]}, yrs, yv, so, 0);
+        else
+          __builtin_amdgcn_raw_buffer_store_b32(h2[0], yrs, yv, so, 0);
+      }
+    return;
+  }
   if (P.nsplit == 1) {
     const bool vec_y = FULL ? (P.vec & 4) != 0 : ((P.vec & 4) != 0 && col0 + CPL <= N);
 #pragma unroll
