@@ -572,8 +572,17 @@ __device__ __forceinline__ void gemm_unpack(const uint32_t (&raw)[4], bf16x8_t (
   }
 }
 
-template <int CPL, bool FULL, int KW>
+// PAIR: a SwiGLU gate/up pair (problem 0 gate, problem 1 up, same shape and
+// activations) in one launch.  Tiles are 128 rows x 128 output columns: waves
+// 0-1 compute the gate's 128 columns and waves 2-3 the up projection's, each
+// as an ordinary 64-column wave sharing the workgroup's activation tile.  The
+// up waves then hand their scaled fp32 tile to the gate waves through the idle
+// activation buffers, and those store bf16(silu(g) * u) from the fp32 sums
+// (engine/llama_mlp.py:30-32).  (Gate and up columns side by side within a
+// lane, with 2-byte weight loads, measured 2.3x slower.)
+template <int CPL, bool FULL, int KW, bool PAIR = false>
 __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))) void gemm_kernel(Launch L) {
+  static_assert(!PAIR || (CPL == 4 && FULL && KW == 1), "the SwiGLU pair GEMM is one shape");
   constexpr int WCOLS = 16 * CPL;       // columns per wave
   constexpr int kATile = 4 * kGemmMT * 64;  // 16-byte entries of one activation tile
   // Two activation buffers [step][subtile][lane] (16 B each) and two row-sum
@@ -595,8 +604,9 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
     wid = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   }
   if (wid >= L.total_wgs) return;
-  const int pi = problem_of(L, wid);
+  const int pi = PAIR ? 0 : problem_of(L, wid);
   const Problem& P = L.p[pi];
+  const Problem& Pw = PAIR ? L.p[__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 7))] : P;  // this wave's weights
   const int tiles = P.tiles_m * P.tiles_n;
   const int local = wid - P.wg_begin;
   const int split = local / tiles;
@@ -619,12 +629,13 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
   const int g_begin = split * P.gps;
   const int g_end = min(G, g_begin + P.gps);
   const int m0 = m_tile * kGemmRows;
-  const int col0 = n_tile * 4 * WCOLS + wave * WCOLS + lc * CPL;
+  // Output column of the lane's first block (a pair: waves w and w + 2 share columns).
+  const int col0 = PAIR ? n_tile * 128 + (wave & 1) * WCOLS + lc * CPL : n_tile * 4 * WCOLS + wave * WCOLS + lc * CPL;
 
   // ---- operand sources ----
-  const uint32_t ldp = (uint32_t)P.ldp;
-  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(P.packed, (uint32_t)((size_t)(P.K / 2) * P.ldp));
-  const __amdgpu_buffer_rsrc_t srs = make_rsrc(P.scale, (uint32_t)((size_t)G * P.lds * 4));
+  const uint32_t ldp = (uint32_t)Pw.ldp;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(Pw.packed, (uint32_t)((size_t)(P.K / 2) * Pw.ldp));
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(Pw.scale, (uint32_t)((size_t)G * Pw.lds * 4));
   const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
   // Activation rows this lane copies (clamped: rows past M compute values that are never stored).
   // Activations come through a buffer resource based at this tile's first
@@ -669,14 +680,14 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
       for (int r = 0; r < 4; ++r) {
         const int64_t pr = (int64_t)g * kPackedRowsPerGroup + st * 16 + lk * 4 + r;
         uint32_t w[1];
-        load_packed<CPL, false>(P.packed + pr * P.ldp, col0, N, (P.vec & 1) != 0, w);
+        load_packed<CPL, false>(Pw.packed + pr * Pw.ldp, col0, N, (P.vec & 1) != 0, w);
         raw[r] = w[0];
       }
     }
   };
   auto load_scales_b = [&](int g, float (&s)[CPL]) {
     if constexpr (FULL) {
-      const uint32_t soff = (uint32_t)g * (uint32_t)P.lds * 4u;
+      const uint32_t soff = (uint32_t)g * (uint32_t)Pw.lds * 4u;
       if constexpr (CPL == 4) {
         const f32x4_t v =
             __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, (uint32_t)col0 * 4u, soff, 0));
@@ -687,7 +698,7 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
         s[0] = v[0]; s[1] = v[1];
       }
     } else {
-      load_scales<CPL, false>(P.scale + (int64_t)g * P.lds, col0, N, (P.vec & 1) != 0, s);
+      load_scales<CPL, false>(Pw.scale + (int64_t)g * Pw.lds, col0, N, (P.vec & 1) != 0, s);
     }
   };
   auto load_b = [&](int g, uint32_t (&raw)[4][4], float (&s)[CPL]) {
@@ -852,6 +863,46 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
   }
 
   // ---- output: lane holds rows m0 + 16i + 4lk + r, columns col0 .. col0+CPL-1 ----
+  if constexpr (PAIR) {
+    // Up waves (2, 3) hand their scaled tile to the gate waves (0, 1) through
+    // the activation buffers: subtiles 0-3 in As0, 4-7 in As1, fragment order.
+    __syncthreads();  // every wave is past its last read of the activation tiles
+    const int half = wave & 1;
+    if (wave >= 2) {
+#pragma unroll
+      for (int i = 0; i < kGemmMT; ++i)
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) {
+          f32x4_t v;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = U[i][t][r] * s_ref[t];
+          u32x4_t* dst = i < kGemmMT / 2 ? As0 : As1;
+          dst[((half * (kGemmMT / 2) + (i % (kGemmMT / 2))) * CPL + t) * 64 + lane] = __builtin_bit_cast(u32x4_t, v);
+        }
+    }
+    __syncthreads();
+    if (wave >= 2) return;
+    // h[m, col0 .. col0 + 3] = bf16(silu(g) * u); y rows are 8-byte aligned (pair_gemm_ok).
+#pragma unroll
+    for (int i = 0; i < kGemmMT; ++i) {
+      f32x4_t u[CPL];
+#pragma unroll
+      for (int t = 0; t < CPL; ++t) {
+        const u32x4_t* src = i < kGemmMT / 2 ? As0 : As1;
+        u[t] = __builtin_bit_cast(f32x4_t, src[((half * (kGemmMT / 2) + (i % (kGemmMT / 2))) * CPL + t) * 64 + lane]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 16 * i + 4 * lk + r;
+        if (m >= M) continue;
+        float h[CPL];
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) h[t] = silu(U[i][t][r] * s_ref[t]) * u[t][r];
+        *reinterpret_cast<u32x2_t*>(P.y + (int64_t)m * P.ldy + col0) = u32x2_t{bf16x2_rne(h[0], h[1]), bf16x2_rne(h[2], h[3])};
+      }
+    }
+    return;
+  }
   if (P.nsplit == 1 && FULL && m0 + kGemmRows <= M && (P.vec & 4) != 0 &&
       (size_t)kGemmRows * P.ldy * 2 < 0xffffffffull) {
     // Whole tile in range: buffer stores off a resource at the tile's first
@@ -1545,6 +1596,63 @@ int workspace_for(const w4a16_problem* probs, int count, size_t* bytes, size_t s
 // half (one grouped launch), then silu_mul_kernel.
 size_t swiglu_up_bytes(const w4a16_problem& q) { return kind_of(q) == kGemv ? 0 : align256((size_t)q.M * q.N * 2); }
 
+// The SwiGLU pair at GEMM-sized M as one gemm_kernel<4, true, 1, true> launch
+// (after the row sums): needs 128-column tiles in range and aligned operands
+// (4-byte weight loads, 16-byte scale loads, 8-byte output stores), and at least
+// one full round of tiles on the chip (there is no split-K in this shape).
+// Otherwise swiglu() runs the grouped GEMM plus silu_mul_kernel.
+bool pair_gemm_ok(const w4a16_problem pair[2]) {
+  const w4a16_problem& g = pair[0];
+  if (kind_of(g) != kGemm || g.N % 128 != 0 || !gemm_x_ok(g)) return false;
+  if ((int64_t)ceil_div(g.M, kGemmRows) * (g.N / 128) < 256) return false;
+  if (!aligned(g.y, 8) || g.ldy % 4 != 0) return false;
+  for (int i = 0; i < 2; ++i) {
+    const w4a16_problem& q = pair[i];
+    if (!aligned(q.packed, 4) || q.ldp % 4 != 0 || !aligned(q.scale, 16) || q.lds % 4 != 0) return false;
+    if ((size_t)(q.K / 2) * q.ldp >= 0xffffffffull || (size_t)(q.K / kGroup) * q.lds * 4 >= 0xffffffffull) return false;
+  }
+  return true;
+}
+
+Plan make_pair_plan(const w4a16_problem pair[2]) {
+  Plan pl{};
+  pl.kind = kGemm;
+  pl.cpl = 4;
+  pl.kw = 1;
+  pl.full = true;
+  pl.pair = true;
+  pl.L.count = 2;
+  for (int i = 0; i < 2; ++i) {
+    const w4a16_problem& q = pair[i];
+    Problem& P = pl.L.p[i];
+    P.x = static_cast<const uint16_t*>(q.x);
+    P.ldx = q.ldx;
+    P.packed = reinterpret_cast<const uint8_t*>(q.packed);
+    P.ldp = q.ldp;
+    P.scale = q.scale;
+    P.lds = q.lds;
+    P.y = static_cast<uint16_t*>(q.y);
+    P.ldy = q.ldy;
+    P.M = q.M;
+    P.N = q.N;
+    P.K = q.K;
+    P.rs_begin = -1;
+    P.nsplit = 1;
+    P.gps = q.K / kGroup;
+    pl.rowsum_src[i] = 0;
+  }
+  Problem& P = pl.L.p[0];
+  P.tiles_m = ceil_div(P.M, kGemmRows);
+  P.tiles_n = P.N / 128;
+  P.rs_begin = 0;
+  pl.rowsum_off[0] = 0;
+  pl.rs_wgs = ceil_div((int64_t)P.M * (P.K / kGroup), 16);
+  pl.ws_bytes = align256((size_t)(P.K / kGroup) * P.M * 4);
+  pl.total_wgs = P.tiles_m * P.tiles_n;
+  pl.L.total_wgs = pl.total_wgs;
+  return pl;
+}
+
 int swiglu(const w4a16_problem pair[2], void* workspace, size_t workspace_bytes, hipStream_t s) {
   const w4a16_problem& g = pair[0];
   if (g.M == 0 || g.N == 0) return W4A16_OK;
@@ -1554,6 +1662,16 @@ int swiglu(const w4a16_problem pair[2], void* workspace, size_t workspace_bytes,
     return launch_status();
   }
   if (kind_of(g) == kGemv) return launch_plan(pair, 2, workspace, workspace_bytes, s, 0, true);
+  if (pair_gemm_ok(pair)) {
+    Plan pl = make_pair_plan(pair);
+    if (!workspace || workspace_bytes < plan_bytes(pl)) return W4A16_ERR_WORKSPACE;
+    bind(pl, workspace, workspace_bytes);
+    hipLaunchKernelGGL(rowsum_kernel, dim3(pl.rs_wgs), dim3(256), 0, s, pl.L);
+    const int rc = launch_status();
+    if (rc != W4A16_OK) return rc;
+    hipLaunchKernelGGL((gemm_kernel<4, true, 1, true>), dim3((pl.total_wgs + 7) & ~7), dim3(256), 0, s, pl.L);
+    return launch_status();
+  }
   const size_t ub = swiglu_up_bytes(g);
   if (!workspace || workspace_bytes < 2 * ub + 256) return W4A16_ERR_WORKSPACE;
   w4a16_problem q[2] = {pair[0], pair[1]};
@@ -1572,9 +1690,13 @@ int swiglu_workspace(const w4a16_problem pair[2], size_t* bytes) {
   const w4a16_problem& g = pair[0];
   if (g.M == 0 || g.N == 0 || g.K == 0) return W4A16_OK;
   if (kind_of(g) == kGemv) return plan_workspace(pair, 2, bytes, 0, true);
+  // Enough for both GEMM-sized forms: the size query sees only shapes, and a
+  // call whose operands are not aligned for the pair kernel takes the grouped
+  // GEMM + silu_mul path.
   const size_t ub = swiglu_up_bytes(g);
   const int rc = workspace_for(pair, 2, bytes, ub);
   *bytes = std::max(*bytes, 2 * ub + 256);
+  if (pair_gemm_ok(pair)) *bytes = std::max(*bytes, plan_bytes(make_pair_plan(pair)));
   return rc;
 }
 

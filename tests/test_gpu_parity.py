@@ -556,10 +556,14 @@ def test_lm_head_qwen3_8b_full_size():
 # by 1, each at most 2^-9 relative, i.e. below ulp(h)/2 per unit, so U = 3.
 # ---------------------------------------------------------------------------
 
-def check_swiglu(h: torch.Tensor, h_ref: np.ndarray, m: int, label: str) -> None:
+def check_swiglu(h: torch.Tensor, h_ref: np.ndarray, m: int, label: str, units: float | None = None) -> None:
+    """max(|h - h_ref| - units * ulp_bf16(h_ref)) <= 1e-3 * RMS.  Fused forms (decode M, and the
+    GEMM pair kernel) round only h: half an ulp.  The grouped GEMM + elementwise form rounds gate
+    and up to bf16 first: 3 ulp."""
     hv = h.float().cpu().numpy().astype(np.float64)
     rms = float(np.sqrt(np.mean(h_ref ** 2)))
-    units = 0.5 if m <= 32 else 3.0
+    if units is None:
+        units = 0.5 if m <= 32 else 3.0
     excess = np.abs(hv - h_ref) - units * ulp_bf16(h_ref)
     say(f"  {label}: rms={rms:.4g} max(excess)/rms={excess.max() / rms:.3e}")
     assert np.isfinite(hv).all(), label
@@ -600,19 +604,39 @@ def test_swiglu_qwen3_8b_full_size(m):
     excess = np.abs(hv - h_ref) - 3.0 * ulp_bf16(h_ref)
     say(f"  vs two int4_matmul: max(excess)/rms={excess.max() / rms:.3e}")
     assert excess.max() <= 1e-3 * rms
-    if m > 32:
-        # Same bf16 gate/up as the separate calls: the epilogue alone differs.
-        # Same bf16 gate/up as the separate calls, so only the epilogue's
-        # fp32 arithmetic and final rounding differ: within one ulp.
-        want = (torch.nn.functional.silu(g.float()) * u.float()).double().cpu().numpy()
-        assert (np.abs(hv - want) <= ulp_bf16(want) + 1e-30).all()
-    else:
-        for _ in range(3):
-            assert torch.equal(int4_swiglu(x, gate, up), h)
-        # sampled columns against the float64 oracle
-        cols = torch.randperm(n, generator=torch.Generator().manual_seed(m))[:48].sort().values.to(DEV)
-        sub = [(p[:, cols].cpu().numpy(), s[:, cols].cpu().numpy()) for p, s in (gate, up)]
-        check_swiglu(h[:, cols], orc.swiglu_reference(x.float().cpu().numpy(), *sub), m, "fp64 oracle, 48 cols")
+    for _ in range(3):
+        assert torch.equal(int4_swiglu(x, gate, up), h)
+    # Sampled columns against the float64 oracle.  Every M here is a fused form (the decode pair,
+    # or at M = 2048 the GEMM pair kernel), which rounds only h: half an ulp.
+    cols = torch.randperm(n, generator=torch.Generator().manual_seed(m))[:48].sort().values.to(DEV)
+    sub = [(p[:, cols].cpu().numpy(), s[:, cols].cpu().numpy()) for p, s in (gate, up)]
+    check_swiglu(h[:, cols], orc.swiglu_reference(x.float().cpu().numpy(), *sub), m, "fp64 oracle, 48 cols",
+                 units=0.5)
+
+
+@pytest.mark.parametrize("m,odd_lds", [(2100, False), (2100, True), (2048, False)])
+def test_swiglu_gemm_pair_kernel_and_fallback(m, odd_lds):
+    """GEMM-sized SwiGLU: the pair kernel (gate and up column blocks in one workgroup, epilogue on
+    fp32 sums) with a partial last row tile, and the grouped GEMM + elementwise fallback that an
+    odd scale row stride selects.  Both against the float64 oracle on sampled columns."""
+    from w4a16 import int4_swiglu, synth
+
+    k, n = 256, 2048  # 17 x 16 tiles of 128 x 128 at M = 2100: one full round and a partial row tile
+    say(f"swiglu gemm pair m={m} odd_lds={odd_lds}")
+    gate = synth.make_weight(k, n, seed=91, device=DEV)
+    up = synth.make_weight(k, n, seed=92, device=DEV)
+    if odd_lds:
+        wide = torch.zeros(k // 128, n + 1, device=DEV)
+        wide[:, :n] = gate[1]
+        gate = (gate[0], wide[:, :n])
+    x = synth.make_activations(m, k, seed=93, device=DEV)
+    h = int4_swiglu(x, gate, up)
+    assert torch.equal(int4_swiglu(x, gate, up), h)
+    cols = torch.randperm(n, generator=torch.Generator().manual_seed(7))[:64].sort().values.to(DEV)
+    sub = [(p[:, cols].cpu().numpy(), s[:, cols].contiguous().cpu().numpy()) for p, s in (gate, up)]
+    ref = orc.swiglu_reference(x.float().cpu().numpy(), *sub)
+    check_swiglu(h[:, cols], ref, m, f"M={m} {'fallback' if odd_lds else 'pair kernel'}",
+                 units=3.0 if odd_lds else 0.5)
 
 
 def test_swiglu_shares_workspace_and_edge_cases():
