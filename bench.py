@@ -20,6 +20,7 @@ The JSON line also carries:
   roofline        decode kernel on gate_proj (K=4096, N=12288, M=1): algorithmic
                   bytes per launch / average launch duration, against 8 TB/s.
   roofline_prefill  the GEMM on gate_proj at M=2048 against dense bf16 MFMA peak.
+  lm_head_M1      the dense bf16 lm_head GEMV at M=1 (Qwen3-8B vocab), GB/s.
   cpu_baseline    the reference's host path (dequantize with bf16 scales, then
                   x @ w in bf16, engine/kernels/quant.py:264-266), restated in
                   oracle/int4_oracle.cpu_path, timed on this host.
@@ -422,6 +423,22 @@ def main() -> int:
     log(f"config 1 (0.6B gate M=1): {us:.2f} us/launch, {config1['GB/s']} GB/s")
     del w1
 
+    # ---- lm_head: the dense bf16 decode GEMV of the untied Qwen3-8B output projection ----
+    from w4a16 import lm_head
+
+    vocab, dmodel = 151936, 4096
+    gen = torch.Generator(device=dev).manual_seed(5)
+    w_lm = (torch.randn(vocab, dmodel, generator=gen, device=dev) * 0.02).bfloat16()
+    x_lm = synth.make_activations(1, dmodel, seed=9, device=dev)
+    us = time_launches(lambda: [lm_head(x_lm, w_lm) for _ in range(LAUNCHES)], stream, reps=3)
+    lm_bytes = vocab * dmodel * 2 + dmodel * 2 + vocab * 2
+    lm = {"workload": "qwen3-8b lm_head M=1 (151936 x 4096 dense bf16, 1.24 GB)", "us": round(us, 2),
+          "GB/s": round(lm_bytes / (us * 1e-6) / 1e9, 1),
+          "frac_of_hbm_peak": round(lm_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    log(f"lm_head M=1: {us:.1f} us/launch, {lm['GB/s']} GB/s")
+    del w_lm
+    torch.cuda.empty_cache()
+
     # ---- config 5: Qwen3-32B, 64-layer M=1 sweep and one M=4096 prefill layer ----
     config5 = None
     if not args.no_32b:
@@ -501,6 +518,7 @@ def main() -> int:
         "batched_decode": batched,
         "prefill": prefill,
         "config1_qwen3_06b": config1,
+        "lm_head_M1": lm,
         "config5_qwen3_32b": config5,
         "roofline": roofline,
         "roofline_prefill": roof_pf,

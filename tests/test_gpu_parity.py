@@ -549,11 +549,13 @@ def test_lm_head_qwen3_8b_full_size():
 # SwiGLU gate/up pair (w4a16_swiglu)
 #
 # Bar: max |h - h64| <= U * ulp_bf16(h64) + 1e-3 * RMS(h64), h64 the float64
-# oracle.  U = 1/2 for M <= 32 (epilogue on the fp32 sums, one bf16 rounding).
-# For larger M gate and up are rounded to bf16 before the epilogue, as in the
-# reference (engine/llama_mlp.py:30-32 rounds each linear output); the rounding
-# of g reaches h scaled by |g silu'(g) / silu(g)| <= 4 and the rounding of u
-# by 1, each at most 2^-9 relative, i.e. below ulp(h)/2 per unit, so U = 3.
+# oracle.  U = 1/2 for the fused forms (the decode pair, and the GEMM pair
+# kernel at GEMM-sized M): epilogue on the fp32 sums, one bf16 rounding.  The
+# fallback at GEMM-sized M (operands not aligned for the pair kernel) rounds
+# gate and up to bf16 before the epilogue, as the reference does
+# (engine/llama_mlp.py:30-32 rounds each linear output); the rounding of g
+# reaches h scaled by |g silu'(g) / silu(g)| <= 4 and the rounding of u by 1,
+# each at most 2^-9 relative, i.e. below ulp(h)/2 per unit, so U = 3.
 # ---------------------------------------------------------------------------
 
 def check_swiglu(h: torch.Tensor, h_ref: np.ndarray, m: int, label: str, units: float | None = None) -> None:
