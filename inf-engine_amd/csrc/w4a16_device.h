@@ -35,6 +35,9 @@ constexpr float kOffset = 136.0f;                // 128 (bf16 base) + 8 (nibble 
 // Cache-policy bit of buffer instructions that makes an access coherent at
 // agent scope across the XCD L2s (the bit agent-scope atomics use).
 constexpr int kAgentCoherent = 16;
+// Cache-policy bit for data read once (non-temporal).  Measured on MI355X over
+// a 1.24 GB stream of 16-byte buffer loads: 6.98 TB/s with it, 6.41 without.
+constexpr int kStream = 2;
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
@@ -107,19 +110,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-template <int BYTES>
+template <int BYTES, int AUX = 0>
 __device__ __forceinline__ void buffer_load_bytes(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                                   uint32_t (&out)[(BYTES + 3) / 4]) {
   if constexpr (BYTES == 16) {
-    const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+    const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));
     out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
   } else if constexpr (BYTES == 8) {
-    const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+    const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, AUX));
     out[0] = v[0]; out[1] = v[1];
   } else if constexpr (BYTES == 4) {
-    out[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    out[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, AUX);
   } else {
-    out[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+    out[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, AUX);
   }
 }
 

@@ -354,6 +354,12 @@ __device__ __forceinline__ void decode_wave(const Problem& P, int g, int col0, i
     }
   }
   if constexpr (FULL) {
+    // Weights and scales are read once per call.  With 128-column strips a
+    // row segment of a lane group is a whole 128-byte line, so the loads are
+    // marked non-temporal (gate M=1 8.55 -> 8.33 us); with 64-column strips
+    // two workgroups share each line and the hint costs a second fetch
+    // (k_proj M=16 5.5 -> 6.5 us), so those keep the default policy.
+    constexpr int kWeightPolicy = CPL == 8 ? kStream : 0;
     const uint32_t ldp = (uint32_t)P.ldp;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(P.packed, (uint32_t)((size_t)(P.K / 2) * P.ldp));
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(P.scale, (uint32_t)((size_t)G * P.lds * 4));
@@ -361,7 +367,7 @@ __device__ __forceinline__ void decode_wave(const Problem& P, int g, int col0, i
 #pragma unroll
     for (int t = 0; t < CPL; t += 4) {
       const f32x4_t v = __builtin_bit_cast(
-          f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, (uint32_t)(col0 + t) * 4u, soff, 0));
+          f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(srs, (uint32_t)(col0 + t) * 4u, soff, kWeightPolicy));
       d.s[t] = v[0]; d.s[t + 1] = v[1]; d.s[t + 2] = v[2]; d.s[t + 3] = v[3];
     }
     const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
@@ -370,7 +376,7 @@ __device__ __forceinline__ void decode_wave(const Problem& P, int g, int col0, i
     for (int st = 0; st < 4; ++st)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        buffer_load_bytes<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, d.raw[st][r]);
+        buffer_load_bytes<CPL, kWeightPolicy>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, d.raw[st][r]);
   } else {
     const bool vw = (P.vec & 1) != 0;
     load_scales<CPL, false>(P.scale + (int64_t)g * P.lds, col0, N, vw, d.s);
@@ -1164,8 +1170,9 @@ __global__ __launch_bounds__(256) void bf16_gemv_rows_kernel(const uint16_t* __r
 #pragma unroll
       for (int sg = 0; sg < kRowSegs; ++sg) {
         const uint32_t off = ((uint32_t)(s0 + sg) * 512u + (uint32_t)lane * 8u) * 2u;  // past K: zeros
-        wv[0][sg] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs0, off, 0, 0));
-        wv[1][sg] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs1, off, 0, 0));
+        // Read-once weights: non-temporal (Qwen3-8B lm_head M=1 226 -> 199 us).
+        wv[0][sg] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs0, off, 0, kStream));
+        wv[1][sg] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs1, off, 0, kStream));
       }
       __builtin_amdgcn_sched_barrier(0);  // all 16 loads in flight before the first dot product
 #pragma unroll
