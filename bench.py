@@ -200,7 +200,7 @@ def roofline_prefill(us: float) -> dict:
         "unit": "TFLOP/s",
         "frac": round(ach / BF16_PEAK_TFLOPS, 4),
         "traffic": read_traffic(TRAFFIC_FILE_PREFILL),
-        "kernel": "gemm_kernel<4, true, 1> (gate_proj K=4096 N=12288 M=2048), after rowsum_kernel",
+        "kernel": "gemm_kernel<4, true, 1, false> (gate_proj K=4096 N=12288 M=2048), after rowsum_kernel",
         "flops_per_launch": f,
         "avg_launch_us": round(us, 3),
     }
