@@ -201,4 +201,12 @@ __device__ __forceinline__ float load_coherent(const float* p) {
 // direct-to-LDS copies) has completed.  gfx9 counts stores in vmcnt.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
+// Wait until at most N of this wave's vector memory operations are still
+// outstanding (loads complete in issue order, so every older one has landed).
+template <int N>
+__device__ __forceinline__ void wait_vmem_n() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
 }  // namespace w4a16

@@ -643,20 +643,16 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
   const __amdgpu_buffer_rsrc_t wrs = make_rsrc(Pw.packed, (uint32_t)((size_t)(P.K / 2) * Pw.ldp));
   const __amdgpu_buffer_rsrc_t srs = make_rsrc(Pw.scale, (uint32_t)((size_t)G * Pw.lds * 4));
   const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
-  // Activation rows this lane copies (clamped: rows past M compute values that are never stored).
   // Activations come through a buffer resource based at this tile's first
-  // row, so every copy is one 32-bit per-lane offset plus a scalar group
-  // offset (no 64-bit address arithmetic per copy).  Rows past M are clamped
-  // to the last row: they compute values that are never stored.
+  // row and ending after its last row inside M, so every copy is one 32-bit
+  // per-lane offset (row lc of subtile 0 plus 16 rows per subtile) and a
+  // scalar group offset.  Rows past M fall outside the resource and read as
+  // zero: they compute values that are never stored.
   const int tile_rows = min(kGemmRows, M - m0);
   const __amdgpu_buffer_rsrc_t xrs =
       make_rsrc(P.x + (int64_t)m0 * P.ldx, (uint32_t)((size_t)tile_rows * P.ldx * 2));
-  uint32_t xv[kGemmMT];
-#pragma unroll
-  for (int i = 0; i < kGemmMT; ++i) {
-    const int row = min(16 * i + lc, tile_rows - 1);
-    xv[i] = ((uint32_t)row * (uint32_t)P.ldx + (uint32_t)((wave * 4 + lk) * 8)) * 2u;
-  }
+  const uint32_t xv0 = ((uint32_t)lc * (uint32_t)P.ldx + (uint32_t)((wave * 4 + lk) * 8)) * 2u;
+  const uint32_t xsub = (uint32_t)P.ldx * 32u;  // bytes per 16-row subtile
   const __amdgpu_buffer_rsrc_t crs = make_rsrc(P.rowsum, (uint32_t)((size_t)G * M * 4));
   const uint32_t cv = (uint32_t)min(m0 + (int)(threadIdx.x & 127), M - 1) * 4u;
 
@@ -666,7 +662,7 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
 #pragma unroll
     for (int i = 0; i < kGemmMT; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (void __attribute__((address_space(3)))*)&as[(wave * kGemmMT + i) * 64],
-                                               16, xv[i], (uint32_t)g * (kGroup * 2), 0, 0);
+                                               16, xv0 + (uint32_t)i * xsub, (uint32_t)g * (kGroup * 2), 0, 0);
     if (wave < 2)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(crs, (void __attribute__((address_space(3)))*)&cs[wave * 64], 4, cv,
                                                (uint32_t)g * (uint32_t)M * 4u, 0, 0);
@@ -720,13 +716,20 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
 #pragma unroll
     for (int t = 0; t < CPL; ++t) U[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Packed weights (4 K steps) and scales of two groups: the group computed
-  // from set BUF while the next one loads into set BUF ^ 1 (the same
-  // compile-time ping-pong as the LDS buffers, so no register copies).
-  // With KW == 2 the two K halves of the workgroup (waves 0-3 and 4-7) take
-  // alternate groups of the range, each with its own LDS buffers, and are
-  // summed through LDS at the end.
-  uint32_t raw2[2][4][4];
+  // Packed weights (4 K steps) and scales.  FULL tiles stream the weights
+  // through one register set: right after step st of a group is unpacked, the
+  // same registers receive step st of the next group, a whole group ahead of
+  // its use.  That keeps 16 VGPRs free for deeper activation prefetch.  Other
+  // tiles (whose loads are not one instruction per row) hold two sets: the
+  // group computed from set BUF while the next one loads into set BUF ^ 1.
+  // Scales always use two sets.  With KW == 2 the two K halves of the
+  // workgroup (waves 0-3 and 4-7) take alternate groups of the range, each
+  // with its own LDS buffers, and are summed through LDS at the end.
+  constexpr bool kStreamB = FULL;
+  // Vector memory operations issued after a group's activation copies: the
+  // next group's scale load and 16 weight loads.
+  constexpr int kLoadsAfterA = 1 + 16;
+  uint32_t raw2[kStreamB ? 1 : 2][4][4];
   float s2[2][CPL];
   float s_ref[CPL];  // scale U is currently expressed in (per column)
   const int g_first = g_begin + kw;
@@ -734,8 +737,16 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
 #pragma unroll
   for (int t = 0; t < CPL; ++t) s_ref[t] = 1.f;
   if (g_first < g_end) {
-    load_b(g_first, raw2[0], s2[0]);
-    stage_a(g_first, std::integral_constant<int, 0>{});
+    if constexpr (kStreamB) {
+      stage_a(g_first, std::integral_constant<int, 0>{});
+      __builtin_amdgcn_sched_barrier(0);
+      load_scales_b(g_first, s2[0]);
+#pragma unroll
+      for (int st = 0; st < 4; ++st) load_b_step(g_first, st, raw2[0][st]);
+    } else {
+      load_b(g_first, raw2[0], s2[0]);
+      stage_a(g_first, std::integral_constant<int, 0>{});
+    }
   }
   W4A16_MARK(1);
   if (g_first < g_end) {
@@ -754,18 +765,28 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
     const int g = g_first + it * KW;
     const u32x4_t* as = a_buf(buf_tag) + kw * kATile;
     const float* cs = c_buf(buf_tag) + kw * kGemmRows;
-    uint32_t (&raw)[4][4] = raw2[b];
+    uint32_t (&raw)[4][4] = raw2[kStreamB ? 0 : b];
     const float (&s)[CPL] = s2[b];
     // Direct-to-LDS copies of this group (issued one iteration earlier) must
-    // have landed before the barrier publishes them.
-    wait_vmem();
+    // have landed before the barrier publishes them.  When the weights stream,
+    // only the loads issued after those copies may still be in flight.
+    if constexpr (kStreamB)
+      wait_vmem_n<kLoadsAfterA>();
+    else
+      wait_vmem();
     __syncthreads();
     if (g >= g_end) return;  // the K half with one group less: barriers only
 
     const bool has_next = g + KW < g_end;
+    const int g_next = has_next ? g + KW : g;
     if (has_next) {
       stage_a(g + KW, std::integral_constant<int, b ^ 1>{});
-      load_b(g + KW, raw2[b ^ 1], s2[b ^ 1]);
+      if constexpr (kStreamB) {
+        __builtin_amdgcn_sched_barrier(0);  // the copies stay ahead of the loads counted above
+        load_scales_b(g + KW, s2[b ^ 1]);
+      } else {
+        load_b(g + KW, raw2[b ^ 1], s2[b ^ 1]);
+      }
     }
 
     // Fold: U <- U * (s_ref / s) - 136 * rowsum.  (U is zero before the first
@@ -798,33 +819,59 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
     // two waves sharing a SIMD fall into alternating unpack / MFMA phases
     // (measured +10% at M = 2048 on q/o/down; no gain with 256-column tiles).
     constexpr bool kStepPrio = CPL == 2;
+    // Activation fragments go through LDS reads one subtile pair ahead of
+    // their MFMAs (pair q = subtiles 2(q%4), 2(q%4)+1 of step q/4), so four
+    // fragments are in flight and each read has a pair's MFMAs to land.
+    // The fences (an empty asm statement for the IR passes, a scheduling
+    // barrier that only VALU and SALU work may cross) keep that order:
+    // without them the compiler sinks every read next to its first use (two
+    // fragments in flight, the wait on the LDS read exposed before every 8
+    // MFMAs).
+    constexpr int kPairs = 4 * kGemmMT / 2;
+    constexpr int kAhead = 1;  // pairs read ahead (2 measured the same, 3 spills)
+    bf16x8_t A[kAhead + 1][2];
+    f32x4_t c4[kAhead + 1][2];
+    auto read_pair = [&](int q, bf16x8_t (&a)[2], f32x4_t (&c)[2]) {
+      const int st = q / (kGemmMT / 2);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int i = 2 * (q % (kGemmMT / 2)) + j;
+        a[j] = __builtin_bit_cast(bf16x8_t, as[(st * kGemmMT + i) * 64 + lane]);
+        if (!kFoldBlock && st == 0) c[j] = *reinterpret_cast<const f32x4_t*>(&cs[16 * i + 4 * lk]);
+      }
+    };
+#pragma unroll
+    for (int q = 0; q < kAhead; ++q) read_pair(q, A[q], c4[q]);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       if constexpr (kStepPrio) __builtin_amdgcn_s_setprio(1);
       bf16x8_t B[CPL];
       gemm_unpack<CPL>(raw[st], B);
-      // Two halves of 4 subtiles: 4 A fragments (and at step 0 the 4 row-sum
-      // vectors) in flight while the previous half's MFMAs issue.
+      // Unconditional (a branch here splits the step and stops the unpack from
+      // interleaving with the MFMAs): the last group re-reads its own rows.
+      // The scheduling barrier keeps the loads here (a group ahead of their
+      // use) while every other kind of instruction may still move across it.
+      if constexpr (kStreamB) {
+        load_b_step(g_next, st, raw[st]);
+        asm volatile("" ::: "memory");  // no IR pass sinks them either
+        __builtin_amdgcn_sched_barrier(0x38F);
+      }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        bf16x8_t A[kGemmMT / 2];
-        f32x4_t c4[kGemmMT / 2];
+      for (int pp = 0; pp < kGemmMT / 2; ++pp) {
+        const int q = st * (kGemmMT / 2) + pp;
+        if (q + kAhead < kPairs) read_pair(q + kAhead, A[(q + kAhead) % (kAhead + 1)], c4[(q + kAhead) % (kAhead + 1)]);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0x6);  // only VALU / SALU work (the unpack) may cross
 #pragma unroll
-        for (int ii = 0; ii < kGemmMT / 2; ++ii) {
-          const int i = h * (kGemmMT / 2) + ii;
-          A[ii] = __builtin_bit_cast(bf16x8_t, as[(st * kGemmMT + i) * 64 + lane]);
-          if (!kFoldBlock && st == 0) c4[ii] = *reinterpret_cast<const f32x4_t*>(&cs[16 * i + 4 * lk]);
-        }
-#pragma unroll
-        for (int ii = 0; ii < kGemmMT / 2; ++ii) {
-          const int i = h * (kGemmMT / 2) + ii;
+        for (int j = 0; j < 2; ++j) {
+          const int i = 2 * pp + j;
 #pragma unroll
           for (int t = 0; t < CPL; ++t) {
             if (!kFoldBlock && st == 0) {
 #pragma unroll
-              for (int r = 0; r < 4; ++r) U[i][t][r] = __builtin_fmaf(U[i][t][r], rho[t], -c4[ii][r]);
+              for (int r = 0; r < 4; ++r) U[i][t][r] = __builtin_fmaf(U[i][t][r], rho[t], -c4[q % (kAhead + 1)][j][r]);
             }
-            U[i][t] = mfma16(A[ii], B[t], U[i][t]);
+            U[i][t] = mfma16(A[q % (kAhead + 1)][j], B[t], U[i][t]);
           }
         }
       }
