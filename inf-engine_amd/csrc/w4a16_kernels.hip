@@ -643,6 +643,7 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
   const __amdgpu_buffer_rsrc_t wrs = make_rsrc(Pw.packed, (uint32_t)((size_t)(P.K / 2) * Pw.ldp));
   const __amdgpu_buffer_rsrc_t srs = make_rsrc(Pw.scale, (uint32_t)((size_t)G * Pw.lds * 4));
   const uint32_t wvoff = (uint32_t)col0 + (uint32_t)(lk * 4) * ldp;
+  const bool w_small = (size_t)(P.K / 2) * Pw.ldp <= 0x80000000ull;
   // Activations come through a buffer resource based at this tile's first
   // row and ending after its last row inside M, so every copy is one 32-bit
   // per-lane offset (row lc of subtile 0 plus 16 rows per subtile) and a
@@ -668,13 +669,13 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
                                                (uint32_t)g * (uint32_t)M * 4u, 0, 0);
   };
   // Packed weights of K step st of group g: 4 packed rows x CPL bytes per lane.
-  auto load_b_step = [&](int g, int st, uint32_t (&raw)[4]) {
+  auto load_b_step = [&](int g, int st, uint32_t (&raw)[4], uint32_t wv) {
     if constexpr (FULL) {
       const uint32_t gbase = (uint32_t)g * kPackedRowsPerGroup * ldp;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         uint32_t w[1];
-        buffer_load_bytes<CPL>(wrs, wvoff, gbase + (uint32_t)(st * 16 + r) * ldp, w);
+        buffer_load_bytes<CPL>(wrs, wv, gbase + (uint32_t)(st * 16 + r) * ldp, w);
         raw[r] = w[0];
       }
     } else {
@@ -705,7 +706,7 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
   };
   auto load_b = [&](int g, uint32_t (&raw)[4][4], float (&s)[CPL]) {
 #pragma unroll
-    for (int st = 0; st < 4; ++st) load_b_step(g, st, raw[st]);
+    for (int st = 0; st < 4; ++st) load_b_step(g, st, raw[st], wvoff);
     load_scales_b(g, s);
   };
 
@@ -742,7 +743,7 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
       __builtin_amdgcn_sched_barrier(0);
       load_scales_b(g_first, s2[0]);
 #pragma unroll
-      for (int st = 0; st < 4; ++st) load_b_step(g_first, st, raw2[0][st]);
+      for (int st = 0; st < 4; ++st) load_b_step(g_first, st, raw2[0][st], wvoff);
     } else {
       load_b(g_first, raw2[0], s2[0]);
       stage_a(g_first, std::integral_constant<int, 0>{});
@@ -778,7 +779,11 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
     if (g >= g_end) return;  // the K half with one group less: barriers only
 
     const bool has_next = g + KW < g_end;
+    // After the last group the streamed loads have nothing to fetch: they go
+    // to offset 2^31, past the weights' resource, and read zero without a
+    // memory access (a resource over more than 2 GB re-reads this group).
     const int g_next = has_next ? g + KW : g;
+    const uint32_t wv_next = (has_next || !w_small) ? wvoff : 0x80000000u;
     if (has_next) {
       stage_a(g + KW, std::integral_constant<int, b ^ 1>{});
       if constexpr (kStreamB) {
@@ -848,11 +853,11 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
       bf16x8_t B[CPL];
       gemm_unpack<CPL>(raw[st], B);
       // Unconditional (a branch here splits the step and stops the unpack from
-      // interleaving with the MFMAs): the last group re-reads its own rows.
+      // interleaving with the MFMAs).
       // The scheduling barrier keeps the loads here (a group ahead of their
       // use) while every other kind of instruction may still move across it.
       if constexpr (kStreamB) {
-        load_b_step(g_next, st, raw[st]);
+        load_b_step(g_next, st, raw[st], wv_next);
         asm volatile("" ::: "memory");  // no IR pass sinks them either
         __builtin_amdgcn_sched_barrier(0x38F);
       }
