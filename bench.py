@@ -16,7 +16,8 @@ The JSON line also carries:
   per_projection  M=1 launch durations per projection.
   batched_decode  config 3: M in {4, 8, 16, 32} at gate/up and down.
   prefill         config 4: the seven projections at M=2048, per projection and
-                  as a layer (drop-in and grouped), TFLOP/s vs 2.5 PFLOP/s.
+                  as a layer (drop-in and grouped), TFLOP/s vs 2.5 PFLOP/s, and
+                  the vendor dense bf16 GEMM on the gate shape for comparison.
   roofline        decode kernel on gate_proj (K=4096, N=12288, M=1): algorithmic
                   bytes per launch / average launch duration, against 8 TB/s.
   roofline_prefill  the GEMM on gate_proj at M=2048 against dense bf16 MFMA peak.
@@ -387,6 +388,17 @@ def main() -> int:
         tf = 2 * synth.algorithmic_flops(m, 4096, 12288) / (us * 1e-6) / 1e12
         proj["swiglu_gate_up"] = {"us": round(us, 2), "TFLOP/s": round(tf, 1)}
         log(f"  prefill swiglu    : {us:8.2f} us  {tf:7.1f} TFLOP/s")
+        # The practical ceiling on this chip: the vendor dense bf16 GEMM
+        # (torch.matmul, hipBLASLt) on the gate shape, same activations, four
+        # distinct N(0, 0.02) bf16 weights (not INT4; no dequantization).
+        gen = torch.Generator(device=dev).manual_seed(7)
+        wd = [torch.randn(4096, 12288, device=dev, dtype=torch.bfloat16, generator=gen).mul_(0.02) for _ in range(4)]
+        us = time_launches(lambda: [xp[4096] @ wd[l % 4] for l in range(LAUNCHES)], stream, reps=3)
+        del wd
+        tf = synth.algorithmic_flops(m, 4096, 12288) / (us * 1e-6) / 1e12
+        dense_ref = {"workload": "dense bf16 torch.matmul (hipBLASLt), M=2048 K=4096 N=12288",
+                     "us": round(us, 2), "TFLOP/s": round(tf, 1)}
+        log(f"  dense bf16 gate (hipBLASLt): {us:8.2f} us  {tf:7.1f} TFLOP/s")
         flops = sum(synth.algorithmic_flops(m, k, n) for _, k, n in shapes)
 
         def layer_fn():
@@ -407,6 +419,7 @@ def main() -> int:
             "workload": "qwen3-8b, M=2048, 7 projections",
             "per_projection": proj,
             "layer": res,
+            "dense_bf16_reference": dense_ref,
             "frac_of_bf16_peak": round(res["drop_in"]["TFLOP/s"] / BF16_PEAK_TFLOPS, 4),
             "peak_tflops": BF16_PEAK_TFLOPS,
         }
