@@ -164,6 +164,42 @@ def test_tolerance_vs_oracle(m, k, n):
     check_tolerance(y, y_ref, f"M={m} K={k} N={n}")
 
 
+# Seeded random shapes across every planner branch: M on both sides of the
+# decode / GEMM boundaries (16, 32, 64), K from one to sixteen groups, N
+# anywhere in 1..2048 (odd, not a multiple of any strip or tile width), with
+# uniform random bytes (nibble -8 included) and, for some cases, strided
+# activation rows and column slices of wider weight / scale tensors.
+SWEEP_SEED = 20261202
+SWEEP_CASES = 32
+
+
+def _sweep_case(i: int):
+    rng = np.random.default_rng(SWEEP_SEED + i)
+    m = int(rng.choice([1, 2, 3, 5, 8, 13, 16, 17, 24, 31, 32, 33, 48, 64, 65, 96, 127, 128, 129, 200, 300]))
+    k = 128 * int(rng.integers(1, 17))
+    n = int(rng.integers(1, 2049))
+    pad_x = int(rng.choice([0, 0, 8, 24]))      # extra activation columns (row stride K + pad)
+    pad_w = int(rng.choice([0, 0, 4, 100]))     # extra weight / scale columns (column slice)
+    return m, k, n, pad_x, pad_w
+
+
+@pytest.mark.parametrize("case", range(SWEEP_CASES))
+def test_random_shape_sweep_vs_oracle(case):
+    from w4a16 import int4_matmul
+
+    m, k, n, pad_x, pad_w = _sweep_case(case)
+    say(f"sweep case={case} m={m} k={k} n={n} pad_x={pad_x} pad_w={pad_w}")
+    g = torch.Generator().manual_seed(SWEEP_SEED + case)
+    packed_full = torch.randint(-128, 128, (k // 2, n + pad_w), generator=g, dtype=torch.int8)
+    scale_full = torch.rand(k // 128, n + pad_w, generator=g) * 0.01 + 0.001
+    x_full = torch.randn(m, k + pad_x, generator=g).to(torch.bfloat16)
+    packed, scale, x = packed_full[:, :n], scale_full[:, :n], x_full[:, :k]
+    y = int4_matmul(x_full.to(DEV)[:, :k], packed_full.to(DEV)[:, :n], scale_full.to(DEV)[:, :n])
+    assert y.shape == (m, n) and y.dtype == torch.bfloat16
+    y_ref = orc.fused_reference(x.float().numpy(), packed.numpy(), scale.numpy())
+    check_tolerance(y, y_ref, f"sweep {case}: M={m} K={k} N={n} pad_x={pad_x} pad_w={pad_w}")
+
+
 @pytest.mark.parametrize("m,k,n", [(1536, 384, 4000), (1536, 640, 4096), (1500, 128, 4096)])
 def test_gemm_two_k_halves(m, k, n):
     """192..256 tiles of 128 x 256: one 8-wave workgroup per tile whose two K
