@@ -200,6 +200,34 @@ def test_random_shape_sweep_vs_oracle(case):
     check_tolerance(y, y_ref, f"sweep {case}: M={m} K={k} N={n} pad_x={pad_x} pad_w={pad_w}")
 
 
+@pytest.mark.parametrize("case", range(12))
+def test_random_grouped_sweep_vs_oracle(case):
+    """int4_matmul_grouped with 1-5 problems: shared activations (one M, one K) or per-problem
+    activations with their own M and K, mixing decode- and GEMM-sized problems in one call."""
+    from w4a16 import int4_matmul_grouped
+
+    rng = np.random.default_rng(SWEEP_SEED + 1000 + case)
+    count = int(rng.integers(1, 6))
+    shared = bool(rng.integers(0, 2))
+    ms = [1, 3, 8, 16, 31, 33, 64, 100, 150, 257]
+    m0, k0 = int(rng.choice(ms)), 128 * int(rng.integers(1, 13))
+    shapes = [(m0, k0) if shared else (int(rng.choice(ms)), 128 * int(rng.integers(1, 13))) for _ in range(count)]
+    ns = [int(rng.integers(1, 1537)) for _ in range(count)]
+    say(f"grouped sweep case={case} shared={shared} problems={[(m, k, n) for (m, k), n in zip(shapes, ns)]}")
+    g = torch.Generator().manual_seed(SWEEP_SEED + 1000 + case)
+    ws = [(torch.randint(-128, 128, (k // 2, n), generator=g, dtype=torch.int8),
+           torch.rand(k // 128, n, generator=g) * 0.01 + 0.001) for (m, k), n in zip(shapes, ns)]
+    xs = [torch.randn(m, k, generator=g).to(torch.bfloat16) for m, k in (shapes[:1] if shared else shapes)]
+    dws = [(p.to(DEV), sc.to(DEV)) for p, sc in ws]
+    ys = int4_matmul_grouped(xs[0].to(DEV) if shared else [x.to(DEV) for x in xs], dws)
+    assert len(ys) == count
+    for i, ((m, k), n) in enumerate(zip(shapes, ns)):
+        x = xs[0] if shared else xs[i]
+        assert ys[i].shape == (m, n)
+        y_ref = orc.fused_reference(x.float().numpy(), ws[i][0].numpy(), ws[i][1].numpy())
+        check_tolerance(ys[i], y_ref, f"grouped {case}.{i}: M={m} K={k} N={n}")
+
+
 @pytest.mark.parametrize("m,k,n", [(1536, 384, 4000), (1536, 640, 4096), (1500, 128, 4096)])
 def test_gemm_two_k_halves(m, k, n):
     """192..256 tiles of 128 x 256: one 8-wave workgroup per tile whose two K
@@ -620,6 +648,23 @@ def test_swiglu_vs_oracle(m, k, n):
     h = int4_swiglu(x.to(DEV), *[(p.to(DEV), s.to(DEV)) for p, s in (gate, up)])
     assert h.shape == (m, n) and h.dtype == torch.bfloat16
     check_swiglu(h, orc.swiglu_reference(x.float().numpy(), gate, up), m, f"swiglu M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("case", range(10))
+def test_random_swiglu_sweep_vs_oracle(case):
+    from w4a16 import int4_swiglu
+
+    rng = np.random.default_rng(SWEEP_SEED + 2000 + case)
+    m = int(rng.choice([1, 2, 7, 16, 25, 32, 40, 64, 65, 130, 300]))
+    k, n = 128 * int(rng.integers(1, 13)), int(rng.integers(1, 1537))
+    say(f"swiglu sweep case={case} m={m} k={k} n={n}")
+    g = torch.Generator().manual_seed(SWEEP_SEED + 2000 + case)
+    gate, up = [(torch.randint(-128, 128, (k // 2, n), generator=g, dtype=torch.int8),
+                 torch.rand(k // 128, n, generator=g) * 0.01 + 0.001) for _ in range(2)]
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    h = int4_swiglu(x.to(DEV), *[(p.to(DEV), sc.to(DEV)) for p, sc in (gate, up)])
+    assert h.shape == (m, n) and h.dtype == torch.bfloat16
+    check_swiglu(h, orc.swiglu_reference(x.float().numpy(), gate, up), m, f"swiglu sweep {case}: M={m} K={k} N={n}")
 
 
 @pytest.mark.parametrize("m", [1, 4, 16, 24, 2048])
