@@ -1415,8 +1415,10 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
     //    than 128 workgroups (k/v projections: more, smaller workgroups), or
     //    when M > 16 (two M subtiles: 103 instead of 140 VGPRs per lane);
     //  * 4 waves per workgroup (one 128-row group each), or 8 when M >= 8,
-    //    when 4 would launch more than 1000 workgroups, or split K more than
-    //    20 ways: past that, reducing inside the workgroup beats more splits;
+    //    when 4 would launch more than 1000 workgroups, or, with M >= 2, split
+    //    K more than 20 ways: past that, reducing inside the workgroup beats
+    //    more splits (Qwen3-8B down at M = 2 / 4: 10.2 / 10.6 -> 9.4 / 9.7 us;
+    //    at M = 1 the 24 splits of 4 waves are faster, 9.07 -> 8.90 us);
     //    and 8 when K has 5..8 groups, so one workgroup covers K and there is
     //    no split-K finish (Qwen3-0.6B gate at M = 1: 3.9 -> 3.4 us).
     int max_m = 0, wg8 = 0, max_split4 = 0, n_odd = 0;
@@ -1432,7 +1434,7 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
     const int wcols = 16 * cpl;
     int wg4 = 0;
     for (int i = 0; i < count; ++i) wg4 += ceil_div(probs[i].N, wcols) * ceil_div(probs[i].K / kGroup, 4);
-    pl.waves = (max_m >= 8 || wg4 > 1000 || max_split4 > 20 || max_split4 == 2) ? 8 : 4;
+    pl.waves = (max_m >= 8 || wg4 > 1000 || (max_split4 > 20 && max_m >= 2) || max_split4 == 2) ? 8 : 4;
     pl.waves = env_int("W4A16_WAVES", pl.waves);
     int wg = 0;
     size_t lds = 0;
