@@ -308,3 +308,121 @@ def test_quantized_to_device_requires_quantized_model():
     model, _ = _mini_model(layers=1)
     with pytest.raises(TypeError):
         quantized_to_device(model, "cpu")
+
+
+# ---------------------------------------------------------------------------
+# Generated-code invariant of the GEMM's streamed weight loads
+# ---------------------------------------------------------------------------
+
+def _gemm_copy_wait_paths(asm: str, func: str) -> list[str]:
+    """Walk the control flow of `func` from every direct-to-LDS copy.
+
+    The GEMM waits for its activation copies with s_waitcnt vmcnt(17): at most
+    17 vector memory operations may still be in flight, which is safe only if
+    at least 17 loads were issued after the copies on every path.  Returns the
+    paths that reach vmcnt(17) or a barrier before any wait that the copies
+    are guaranteed to satisfy (vmcnt(n) after >= n later loads).
+    """
+    start = asm.index(func + ":")
+    body = asm[start:asm.index(".Lfunc_end", start)].splitlines()[1:]
+    blocks, order, cur = {}, [], "entry"
+    blocks[cur] = []
+    order.append(cur)
+    for line in body:
+        t = line.split(";")[0].strip()
+        if not t:
+            continue
+        if re.match(r"^\.LBB\w+:$", t):
+            cur = t[:-1]
+            blocks[cur] = []
+            order.append(cur)
+            continue
+        op = t.split()[0]
+        if op.startswith("buffer_load") or op.startswith("global_load"):
+            blocks[cur].append(("C",) if t.endswith(" lds") else ("L",))
+        elif op == "s_waitcnt" and "vmcnt(" in t:
+            blocks[cur].append(("W", int(re.search(r"vmcnt\((\d+)\)", t).group(1))))
+        elif op == "s_barrier":
+            blocks[cur].append(("B",))
+        elif op == "s_branch":
+            blocks[cur].append(("J", t.split()[-1]))
+        elif op.startswith("s_cbranch"):
+            blocks[cur].append(("CJ", t.split()[-1]))
+        elif op == "s_endpgm":
+            blocks[cur].append(("E",))
+    nxt = {b: (order[i + 1] if i + 1 < len(order) else None) for i, b in enumerate(order)}
+    bad = []
+
+    def walk(block, idx, count, seen):
+        key = (block, idx, min(count, 17))
+        if key in seen:
+            return
+        seen.add(key)
+        ins = blocks[block]
+        for j in range(idx, len(ins)):
+            e = ins[j]
+            if e[0] == "C":
+                return  # the walk from that copy covers the rest
+            if e[0] == "L":
+                count += 1
+            elif e[0] == "W":
+                if count >= e[1]:
+                    return  # the copies are complete here
+                if e[1] == 17:
+                    bad.append(f"{block}: vmcnt(17) after {count} loads")
+                    return
+            elif e[0] == "B":
+                bad.append(f"{block}: barrier after {count} loads, copies not waited for")
+                return
+            elif e[0] == "E":
+                return
+            elif e[0] == "J":
+                walk(e[1], 0, count, seen)
+                return
+            elif e[0] == "CJ":
+                walk(e[1], 0, count, seen)
+        if nxt[block] is not None:
+            walk(nxt[block], 0, count, seen)
+
+    for b in order:
+        for i, e in enumerate(blocks[b]):
+            if e[0] == "C":
+                walk(b, i + 1, 0, set())
+    return bad
+
+
+def test_gemm_streamed_loads_cover_the_copy_wait(tmp_path):
+    """Every full-tile GEMM instantiation issues >= 17 loads between its activation copies and
+    the vmcnt(17) wait that publishes them (the source's kLoadsAfterA), on every path."""
+    import shutil
+    import subprocess
+    import sys
+
+    from w4a16 import build as B
+
+    if not os.path.exists(B.HIPCC) and shutil.which("hipcc") is None:
+        pytest.skip("hipcc not available")
+    out = tmp_path / "k.s"
+    flags = [f for f in B.FLAGS if f not in ("-fPIC", "-shared")]
+    res = subprocess.run([B.HIPCC, *flags, "--cuda-device-only", "-S", *B.SOURCES, "-o", str(out)],
+                         capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    asm = out.read_text()
+    funcs = sorted(set(re.findall(r"^(_Z\w*gemm_kernelILi\dELb1E\w*):", asm, re.M)))
+    assert len(funcs) >= 4, funcs  # CPL 2 / 4, two K halves, the SwiGLU pair
+    for f in funcs:
+        assert "vmcnt(17)" in asm[asm.index(f + ":"):asm.index(".Lfunc_end", asm.index(f + ":"))], f
+        bad = _gemm_copy_wait_paths(asm, f)
+        assert not bad, (f, bad[:5])
+        print(f, "ok", file=sys.stderr)
+
+
+def test_gemm_copy_wait_walker_flags_short_paths():
+    """The walker itself: 16 loads before vmcnt(17) is a race, 17 is not, through a loop."""
+    def fake(nloads):
+        loads = "\n".join("\tbuffer_load_dword v1, v2, s[0:3], s4 offen" for _ in range(nloads))
+        return (f"fn:\n\tbuffer_load_dwordx4 v3, s[0:3], s5 offen lds\n{loads}\n.LBB0_1:\n"
+                f"\ts_waitcnt vmcnt(17)\n\ts_barrier\n\tbuffer_load_dwordx4 v3, s[0:3], s5 offen lds\n{loads}\n"
+                "\ts_cbranch_scc1 .LBB0_1\n\ts_endpgm\n.Lfunc_end0:\n")
+    assert _gemm_copy_wait_paths(fake(17), "fn") == []
+    assert _gemm_copy_wait_paths(fake(16), "fn")
