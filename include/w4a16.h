@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 5
+#define W4A16_ABI_VERSION 6
 
 /* Most problems one grouped call accepts. */
 #define W4A16_MAX_PROBLEMS 16
@@ -41,6 +41,10 @@ extern "C" {
 #define W4A16_ERR_DTYPE 7       /* unknown dtype code */
 #define W4A16_ERR_TOO_LARGE 8   /* problem exceeds what the entry point supports (w4a16_bf16_gemv: M > 16;
                                    decode-sized M whose split-K partials, nsplit * M * N * 4 bytes, reach 4 GB) */
+
+/* Bits of a workspace's status word (see w4a16_status_offset). */
+#define W4A16_STATUS_SPLITK_TIMEOUT 1u  /* a decode split-K finisher gave up polling: its outputs are NaN and
+                                           the workspace's slot half may hold stale partials (zero it again) */
 
 /* dtype codes for w4a16_dequant. */
 #define W4A16_DTYPE_F32 0
@@ -79,9 +83,10 @@ const char* w4a16_error_string(int code);
  * every completed call; the upper half is GEMM scratch.  So: zero a buffer
  * once when it is allocated, pass its full size on every call, and replace it
  * by a new zeroed buffer to grow it.  Calls that share a workspace must be
- * ordered (same stream).  Replaces no reference entry point: the reference
- * kernel needs no workspace (engine/kernels/quant.py:270-280 allocates only
- * the output).
+ * ordered (same stream).  The last aligned 32-bit word of the workspace is its
+ * status word (w4a16_status_offset).  Replaces no reference entry point: the
+ * reference kernel needs no workspace (engine/kernels/quant.py:270-280
+ * allocates only the output).
  */
 int w4a16_workspace_size(int M, int N, int K, int group_size, size_t* bytes);
 
@@ -126,6 +131,25 @@ int w4a16_linear(const void* x, int64_t ldx,
 int w4a16_linear_grouped(const w4a16_problem* problems, int count, int group_size,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Byte offset of the status word inside a workspace of workspace_bytes bytes
+ * (the last aligned 32-bit word; workspaces under 256 bytes have none and
+ * return W4A16_ERR_WORKSPACE).  It is zero as allocated; a decode split-K
+ * finisher that exhausts its poll budget ORs W4A16_STATUS_SPLITK_TIMEOUT into
+ * it (and writes NaN outputs).  Read it after synchronising the stream; when
+ * it is set, zero the whole workspace before its next use.  No counterpart in
+ * the reference, whose kernel has no cross-workgroup protocol.
+ */
+int w4a16_status_offset(size_t workspace_bytes, size_t* offset);
+
+/*
+ * Poll budget of the decode split-K finisher for later calls in this process
+ * (default 2^20 rounds; returns the previous value).  For tests of the
+ * give-up path: a budget of 0 makes a finisher give up as soon as one of its
+ * slots is still empty, so every kernel still ends normally.
+ */
+uint32_t w4a16_debug_set_spin_limit(uint32_t polls);
+
 /* Workspace bytes w4a16_linear_grouped needs for this problem table. */
 int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int group_size, size_t* bytes);
 
@@ -139,8 +163,12 @@ int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int g
  * launches plus two elementwise kernels.  Decode-sized M (as in w4a16_linear) runs one decode launch that
  * streams both weights and applies the epilogue to the fp32 sums (the
  * reference rounds gate and up to bf16 first; results agree to bf16 rounding).
- * Larger M computes gate into h and up into workspace, then one elementwise
- * pass.  Status codes, group_size and workspace rules as w4a16_linear, with
+ * GEMM-sized M runs the row sums and then one pair GEMM launch whose
+ * workgroups compute matching gate and up tiles and store silu(g) * u from
+ * the fp32 sums.  Operands the pair GEMM cannot take (N not a multiple of
+ * 128, fewer than 256 tiles, unaligned rows) go through a grouped GEMM (gate
+ * into h, up into workspace) and one elementwise pass.  Status codes,
+ * group_size and workspace rules as w4a16_linear, with
  * w4a16_workspace_size_swiglu() in place of w4a16_workspace_size().
  */
 int w4a16_swiglu(const void* x, int64_t ldx,

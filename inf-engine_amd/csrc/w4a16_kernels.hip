@@ -19,12 +19,13 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
-#include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "../../include/w4a16.h"
+#include "slot_protocol.h"
 #include "w4a16_device.h"
 
 using namespace w4a16;
@@ -32,7 +33,7 @@ using namespace w4a16;
 namespace {
 
 constexpr int kMaxProblems = W4A16_MAX_PROBLEMS;
-constexpr uint32_t kSpinLimit = 1u << 20;      // polls before a finishing workgroup gives up (writes NaN)
+static_assert(kStatusSplitKTimeout == W4A16_STATUS_SPLITK_TIMEOUT, "status bit of the C ABI");
 
 // One projection of a launch, as the device sees it.
 struct Problem {
@@ -61,23 +62,10 @@ struct Launch {
   Problem p[kMaxProblems];
   int count;
   int total_wgs;
-#ifdef W4A16_EXP
-  uint64_t* trace;     // per-wave phase timestamps (experiments only)
-#endif
+  uint32_t* status;    // the workspace's status word (W4A16_STATUS_*), or null without a workspace
+  uint32_t spin_limit; // polls before a split-K finisher gives up
 };
 
-#ifdef W4A16_EXP
-#define W4A16_MARK(i)                                                                                     \
-  do {                                                                                                    \
-    if (L.trace && (threadIdx.x & 63) == 0)                                                               \
-      L.trace[(((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6)) * 8 + (i)] = \
-          __builtin_amdgcn_s_memrealtime();                                                               \
-  } while (0)
-#else
-#define W4A16_MARK(i) \
-  do {                \
-  } while (0)
-#endif
 
 // Problem owning workgroup `wg` (wave-uniform scan of <= 8 entries).
 __device__ __forceinline__ int problem_of(const Launch& L, int wg) {
@@ -91,30 +79,25 @@ __device__ __forceinline__ int problem_of(const Launch& L, int wg) {
 // Split-K reduction of the decode kernel, without atomics.
 //
 // The workgroup of the last split (split == nsplit - 1) of a strip finishes
-// it; the others publish their fp32 partial and exit.  A published slot holds
-// the bitwise complement of the partial, so a slot reading 0 is still empty
-// (the one partial whose complement is 0, the NaN 0xFFFFFFFF, is published as
-// the canonical NaN 0x7FC00000).  The finisher polls the nsplit - 1 slots of
-// each of its elements with agent-coherent loads, sums them in split order
-// with its own partial last (deterministic), writes bf16 and zeroes the slots
-// again, so the slots are empty at the start of every call.
+// it; the others publish their fp32 partial and exit.  Slot encoding, the
+// empty test and the give-up rule are in slot_protocol.h: a slot reading 0 is
+// still empty, published slots hold the complement of the partial.  The
+// finisher polls the nsplit - 1 slots of each of its elements with
+// agent-coherent loads, sums them in split order with its own partial last
+// (deterministic), writes bf16 and zeroes the slots again, so the slots are
+// empty at the start of every call.
 //
 // Why no workgroup can wait forever: the grid orders workgroups split-major
 // ((strip, split) grids, or split-major ids within a problem), so a finisher
 // is dispatched after every workgroup it waits for, and those never wait on
-// anything.  The poll is still bounded (kSpinLimit); a finisher that gives up
-// writes NaN, so a failure is visible rather than a hang.
+// anything.  The poll is still bounded (Launch::spin_limit); a finisher that
+// gives up writes NaN and sets kStatusSplitKTimeout in the workspace status
+// word, which the host reads after a synchronisation.
 //
 // An arrival counter instead (one agent-scope atomic per workgroup, the last
 // arrival reduces) measures 1 us (8 splits) to 3.3 us (24 splits) slower per
 // launch on MI355X: atomics on one address serialize.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t publish_bits(float v) {
-  uint32_t b = __float_as_uint(v);
-  if (b == 0xffffffffu) b = 0x7fc00000u;
-  return ~b;
-}
-
 // Poll-and-sum of nslots published slots (stride bytes apart) for a
 // thread's EPT elements at byte offsets off[].  All of a thread's polls for a
 // chunk of SCH slots are in flight at once, so a thread with several elements
@@ -131,7 +114,7 @@ __device__ __forceinline__ uint32_t publish_bits(float v) {
 template <int EPT>
 __device__ __forceinline__ void sum_slots(__amdgpu_buffer_rsrc_t rs, int nslots, uint32_t stride,
                                           const uint32_t (&off)[EPT], const bool (&ok)[EPT], float (&v)[EPT],
-                                          bool& timed_out) {
+                                          uint32_t limit, bool& timed_out) {
   constexpr int SCH = EPT >= 8 ? 2 : (EPT >= 4 ? 4 : 8);  // slots per chunk: EPT * SCH polls in flight
   for (int sp0 = 0; sp0 < nslots; sp0 += SCH) {
     uint32_t t[EPT][SCH];
@@ -141,7 +124,7 @@ __device__ __forceinline__ void sum_slots(__amdgpu_buffer_rsrc_t rs, int nslots,
       for (int i = 0; i < SCH; ++i)
         t[j][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, off[j] + (uint32_t)(sp0 + i) * stride, 0, kAgentCoherent);
     // A slot is still empty when it reads 0, lies within nslots and belongs to one of our elements.
-    auto empty = [&](int j, int i) { return t[j][i] == 0u && sp0 + i < nslots && ok[j]; };
+    auto empty = [&](int j, int i) { return slot_empty(t[j][i]) && sp0 + i < nslots && ok[j]; };
     // Wave-uniform loop: every round re-polls all SCH slots and keeps the
     // ones that had already arrived.
     for (uint32_t spins = 0;; ++spins) {
@@ -151,7 +134,7 @@ __device__ __forceinline__ void sum_slots(__amdgpu_buffer_rsrc_t rs, int nslots,
 #pragma unroll
         for (int i = 0; i < SCH; ++i) missing = missing | empty(j, i);  // bitwise: no short-circuit branches
       if (__builtin_amdgcn_ballot_w64(missing) == 0) break;
-      if (spins == kSpinLimit) {
+      if (spins >= limit) {
         timed_out = true;
         break;
       }
@@ -169,7 +152,7 @@ __device__ __forceinline__ void sum_slots(__amdgpu_buffer_rsrc_t rs, int nslots,
 #pragma unroll
     for (int j = 0; j < EPT; ++j)
 #pragma unroll
-      for (int i = 0; i < SCH; ++i) v[j] += sp0 + i < nslots ? __uint_as_float(~t[j][i]) : 0.f;
+      for (int i = 0; i < SCH; ++i) v[j] += sp0 + i < nslots ? slot_value(t[j][i]) : 0.f;
   }
 #pragma unroll
   for (int j = 0; j < EPT; ++j)
@@ -190,8 +173,8 @@ enum FinishMode {
 
 // EPT: most elements (rows x columns of the strip) one thread handles.
 template <int NT, int EPT, int MODE, class PartialFn>
-__device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split, int n0, int wcols, int rows,
-                                              PartialFn partial, const Problem* gate = nullptr) {
+__device__ __forceinline__ void splitk_finish(const Launch& L, const Problem& P, int M, int split, int n0, int wcols,
+                                              int rows, PartialFn partial, const Problem* gate = nullptr) {
   const int N = P.N;
   const int elems = rows * wcols;
   // Slots are [nslots][M][N] fp32; byte offsets fit in 32 bits (make_plan).
@@ -222,13 +205,14 @@ __device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split
     v[j] = 0.f;
   }
   bool timed_out = false;
-  sum_slots<EPT>(rs, last, stride, off, ok, v, timed_out);
+  const uint32_t limit = L.spin_limit;
+  sum_slots<EPT>(rs, last, stride, off, ok, v, limit, timed_out);
   if constexpr (MODE == kFinishUp) {
     float gv[EPT];
 #pragma unroll
     for (int j = 0; j < EPT; ++j) gv[j] = 0.f;
     const __amdgpu_buffer_rsrc_t grs = make_rsrc(gate->part, stride * (uint32_t)gate->nsplit);
-    sum_slots<EPT>(grs, gate->nsplit, stride, off, ok, gv, timed_out);
+    sum_slots<EPT>(grs, gate->nsplit, stride, off, ok, gv, limit, timed_out);
 #pragma unroll
     for (int j = 0; j < EPT; ++j) v[j] = silu(gv[j]) * (v[j] + own[j]);
   } else {
@@ -242,6 +226,9 @@ __device__ __forceinline__ void splitk_finish(const Problem& P, int M, int split
     const int m = e / wcols, n = n0 + e % wcols;
     P.y[(int64_t)m * P.ldy + n] = timed_out ? (uint16_t)0x7fc0 : f32_to_bf16(v[j]);
   }
+  // timed_out is wave-uniform (it follows a ballot); one lane per wave reports it.
+  if (timed_out && (threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_or(L.status, kStatusSplitKTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -434,7 +421,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
   const int G = (uint32_t)P.K / kGroup;
   const int g = split * P.gps + wave;
   const bool active = wave < P.gps && g < G;  // wave-uniform
-  W4A16_MARK(0);
 
   constexpr int MT = (MROWS + 15) / 16;
   f32x4_t total[MT][CPL];
@@ -443,7 +429,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
 #pragma unroll
     for (int t = 0; t < CPL; ++t) total[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   if (active) decode_wave<CPL, FULL, MT>(P, g, col0, lc, lk, M, total);
-  W4A16_MARK(3);
 
   // Reduce the waves through LDS.  Rows m = 16*mt + 4*lk + r of the MFMA output.
   float* red = smem;
@@ -461,7 +446,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
       }
     }
   __syncthreads();
-  W4A16_MARK(4);
   const int elems = M * WCOLS;
   auto wave_sum = [&](int e) {
     float v = red[e];
@@ -472,9 +456,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
   constexpr int EPT = (MROWS * WCOLS + NT - 1) / NT;
   if constexpr (PAIR) {
     if (pi == 0)
-      splitk_finish<NT, EPT, kFinishGate>(P, M, split, n0, WCOLS, M, wave_sum);
+      splitk_finish<NT, EPT, kFinishGate>(L, P, M, split, n0, WCOLS, M, wave_sum);
     else
-      splitk_finish<NT, EPT, kFinishUp>(P, M, split, n0, WCOLS, M, wave_sum, &L.p[0]);
+      splitk_finish<NT, EPT, kFinishUp>(L, P, M, split, n0, WCOLS, M, wave_sum, &L.p[0]);
     return;
   }
   if (P.nsplit == 1) {
@@ -482,11 +466,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(Launch L) {
       const int m = e / WCOLS, c = e % WCOLS, n = n0 + c;
       if (n < N) P.y[(int64_t)m * P.ldy + n] = f32_to_bf16(wave_sum(e));
     }
-    W4A16_MARK(5);
     return;
   }
-  splitk_finish<NT, EPT, kFinishStore>(P, M, split, n0, WCOLS, M, wave_sum);
-  W4A16_MARK(6);
+  splitk_finish<NT, EPT, kFinishStore>(L, P, M, split, n0, WCOLS, M, wave_sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -710,7 +692,6 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
     load_scales_b(g, s);
   };
 
-  W4A16_MARK(0);
   f32x4_t U[kGemmMT][CPL];
 #pragma unroll
   for (int i = 0; i < kGemmMT; ++i)
@@ -749,7 +730,6 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
       stage_a(g_first, std::integral_constant<int, 0>{});
     }
   }
-  W4A16_MARK(1);
   if (g_first < g_end) {
 #pragma unroll
     for (int t = 0; t < CPL; ++t) s_ref[t] = clamp_scale(s2[0][t]);
@@ -1011,7 +991,6 @@ __global__ __launch_bounds__(256 * KW) __attribute__((amdgpu_waves_per_eu(2, 8))
     return;
   }
 
-  W4A16_MARK(3);
   // ---- K split: store this split's fp32 tile (already scaled); splitk_reduce_kernel
   // sums the splits in order in the next launch ----
   float* part = P.part + (size_t)split * M * N;
@@ -1320,15 +1299,6 @@ inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-int env_int(const char* name, int dflt) {
-#ifdef W4A16_EXP
-  const char* v = getenv(name);
-  if (v) return atoi(v);
-#endif
-  (void)name;
-  return dflt;
-}
-
 struct Plan {
   Kind kind;
   int cpl;
@@ -1367,9 +1337,8 @@ bool gemm_x_ok(const w4a16_problem& q) { return aligned(q.x, 16) && q.ldx % 8 ==
 // and 64: Qwen3-8B q/k 1.6-1.8x faster than the GEMM, gate/down within 10%,
 // Qwen3-32B gate/down 1.2-1.7x slower).
 inline Kind kind_of(const w4a16_problem& q) {
-  static const int gemv_max = env_int("W4A16_GEMV_MAX", 64);
-  if (q.M <= 32 && q.M <= gemv_max) return kGemv;
-  if (q.M > gemv_max) return kGemm;
+  if (q.M <= 32) return kGemv;
+  if (q.M > 64) return kGemm;
   const int64_t wgs = (int64_t)ceil_div(q.N, 64) * ceil_div(q.K / kGroup, 8);
   return wgs <= 1024 ? kGemv : kGemm;
 }
@@ -1429,13 +1398,12 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
       max_split4 = std::max(max_split4, ceil_div(G, 4));
       n_odd += probs[i].N % 128 != 0;
     }
-    const int cpl = env_int("W4A16_CPL", (n_odd > 0 || wg8 < 128 || max_m > 16) ? 4 : 8);
+    const int cpl = (n_odd > 0 || wg8 < 128 || max_m > 16) ? 4 : 8;
     pl.cpl = cpl;
     const int wcols = 16 * cpl;
     int wg4 = 0;
     for (int i = 0; i < count; ++i) wg4 += ceil_div(probs[i].N, wcols) * ceil_div(probs[i].K / kGroup, 4);
     pl.waves = (max_m >= 8 || wg4 > 1000 || (max_split4 > 20 && max_m >= 2) || max_split4 == 2) ? 8 : 4;
-    pl.waves = env_int("W4A16_WAVES", pl.waves);
     int wg = 0;
     size_t lds = 0;
     for (int i = 0; i < count; ++i) {
@@ -1474,8 +1442,8 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
     //    4-wave workgroups per CU do better (32B down 674 vs 799 us).
     int t4 = 0;
     for (int i = 0; i < count; ++i) t4 += ceil_div(probs[i].M, kGemmRows) * ceil_div(probs[i].N, 256);
-    pl.cpl = env_int("W4A16_GCPL", t4 < 192 ? 2 : 4);
-    pl.kw = env_int("W4A16_GKW", pl.cpl == 4 && t4 <= 256 ? 2 : 1);
+    pl.cpl = t4 < 192 ? 2 : 4;
+    pl.kw = pl.cpl == 4 && t4 <= 256 ? 2 : 1;
     if (pl.cpl == 2) pl.kw = 1;
     const int tcols = 64 * pl.cpl;
     int tiles_total = 0;
@@ -1492,7 +1460,6 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
       // keeping >= 4 groups per split.
       int nsplit = tiles_total >= 384 ? 1 : std::max(1, 512 / tiles_total);
       nsplit = std::min(nsplit, std::max(1, G / 4));
-      nsplit = env_int("W4A16_GSPLIT", nsplit);
       if (pl.cpl == 4) nsplit = 1;  // 256-column tiles only when the chip is already full
       while (nsplit > 1 && (size_t)nsplit * M * P.N * 4 >= 0xffffffffull) --nsplit;  // 32-bit buffer offsets
       P.gps = ceil_div(G, nsplit);
@@ -1536,9 +1503,22 @@ Plan make_plan(const w4a16_problem* probs, int count, bool pair = false) {
 // read), and the GEMM's row sums and split partials in the upper half, which
 // holds garbage after a GEMM.  Keeping them apart is what lets the decode
 // slots rely on "0 = empty" whatever ran before on the same workspace.
+//
+// The last aligned 32-bit word of the workspace is its status word
+// (kStatusSplitKTimeout), zero as allocated; plan_bytes() leaves the last 128
+// bytes outside both halves' scratch, so nothing else writes it.
+std::atomic<uint32_t> g_spin_limit{kDefaultSpinLimit};
+
+uint32_t* status_word(void* workspace, size_t workspace_bytes) {
+  if (!workspace || workspace_bytes < 256) return nullptr;
+  return reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + ((workspace_bytes - 4) & ~(size_t)3));
+}
+
 void bind(Plan& pl, void* workspace, size_t workspace_bytes) {
   char* ws = static_cast<char*>(workspace);
   char* upper = ws + ((workspace_bytes / 2) & ~(size_t)255) + pl.skip;
+  pl.L.status = status_word(workspace, workspace_bytes);
+  pl.L.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   for (int i = 0; i < pl.L.count; ++i) {
     Problem& P = pl.L.p[i];
     if (pl.kind == kGemm) {
@@ -1548,10 +1528,6 @@ void bind(Plan& pl, void* workspace, size_t workspace_bytes) {
       P.part = reinterpret_cast<float*>(ws + pl.part_off[i]);
     }
   }
-#ifdef W4A16_EXP
-  pl.L.trace = getenv("W4A16_TRACE") ? reinterpret_cast<uint64_t*>(strtoull(getenv("W4A16_TRACE"), nullptr, 0))
-                                     : nullptr;
-#endif
 }
 
 // Workspace bytes a plan needs: twice its half, rounded.  The GEMM scratch
@@ -1895,6 +1871,15 @@ int w4a16_workspace_size(int M, int N, int K, int group_size, size_t* bytes) {
                         reinterpret_cast<const float*>(a), N, reinterpret_cast<void*>(a), N, M, N, K};
   return workspace_for(&q, 1, bytes);
 }
+
+int w4a16_status_offset(size_t workspace_bytes, size_t* offset) {
+  if (!offset) return W4A16_ERR_NULL;
+  if (workspace_bytes < 256) return W4A16_ERR_WORKSPACE;
+  *offset = (workspace_bytes - 4) & ~(size_t)3;
+  return W4A16_OK;
+}
+
+uint32_t w4a16_debug_set_spin_limit(uint32_t polls) { return g_spin_limit.exchange(polls); }
 
 int w4a16_workspace_size_grouped(const w4a16_problem* problems, int count, int group_size, size_t* bytes) {
   if (!bytes) return W4A16_ERR_NULL;

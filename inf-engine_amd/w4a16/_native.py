@@ -26,6 +26,11 @@ W4A16_ERR_LAUNCH = 6
 W4A16_ERR_DTYPE = 7
 W4A16_ERR_TOO_LARGE = 8
 
+W4A16_STATUS_SPLITK_TIMEOUT = 1
+
+# W4A16_ABI_VERSION of include/w4a16.h this binding is written against.
+ABI_VERSION = 6
+
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
@@ -43,6 +48,8 @@ EXPORTED_SYMBOLS = (
     "w4a16_bf16_gemv",
     "w4a16_swiglu",
     "w4a16_workspace_size_swiglu",
+    "w4a16_status_offset",
+    "w4a16_debug_set_spin_limit",
 )
 
 
@@ -82,6 +89,16 @@ def load_library() -> ctypes.CDLL:
         i64, i32, vp, sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
         lib.w4a16_abi_version.argtypes = []
         lib.w4a16_abi_version.restype = i32
+        built = lib.w4a16_abi_version()
+        if built != ABI_VERSION:
+            raise NativeLibraryMissing(
+                f"{LIB_PATH} implements ABI version {built}, this package expects {ABI_VERSION}: "
+                "the library is stale (python -c 'import __graft_entry__ as g; g.build()')"
+            )
+        lib.w4a16_status_offset.argtypes = [sz, ctypes.POINTER(sz)]
+        lib.w4a16_status_offset.restype = i32
+        lib.w4a16_debug_set_spin_limit.argtypes = [ctypes.c_uint32]
+        lib.w4a16_debug_set_spin_limit.restype = ctypes.c_uint32
         lib.w4a16_error_string.argtypes = [i32]
         lib.w4a16_error_string.restype = ctypes.c_char_p
         lib.w4a16_workspace_size.argtypes = [i32, i32, i32, i32, ctypes.POINTER(sz)]
@@ -145,32 +162,108 @@ def workspace_size(m: int, n: int, k: int, group_size: int = 128) -> int:
     return out.value
 
 
-# One zeroed workspace per (device, stream).  Its lower half holds the decode
-# kernels' split-K partial slots, which every call leaves at zero, so a buffer
-# is only zeroed when it is (re)allocated; the full size is passed on every call.  Calls on one stream are ordered, which is
-# what makes sharing the buffer safe.
-_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+# Split-K workspaces.
+#
+# One zero-initialised buffer per (device, stream): calls on one stream are
+# ordered, which is what makes sharing a buffer safe (the decode kernels'
+# published-partial slots are empty again when every call ends).  The full
+# size is passed on every call.
+#
+# HIP graphs bake the workspace pointer into their kernel nodes, so a buffer
+# that any capture has used is never freed: when it is outgrown it moves to
+# `_retired` and stays allocated for the life of the process.  A stream that
+# first needs a workspace while it is capturing (torch.cuda.graph captures on
+# its own side stream after the caller warmed up on another one) gets a buffer
+# allocated inside the capture, from the graph's memory pool; its zero fill is
+# a fill kernel recorded into the graph, so every replay starts from empty
+# slots.  Until a replay has run, such a buffer holds no defined data, so an
+# eager call on that stream first zeroes it.
+class _Workspace:
+    __slots__ = ("tensor", "captured", "defined")
+
+    def __init__(self, tensor: torch.Tensor, captured: bool, defined: bool):
+        self.tensor = tensor
+        self.captured = captured   # some captured graph holds this buffer's address
+        self.defined = defined     # contents are known to be zero / valid for eager use
+
+
+_workspaces: dict[tuple[int, int], _Workspace] = {}
+_retired: list[torch.Tensor] = []
 _ws_lock = threading.Lock()
+_MIN_WORKSPACE = 1 << 20
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
 
 
 def get_workspace(device: torch.device, stream_handle: int, nbytes: int) -> torch.Tensor | None:
+    """The workspace of (device, stream), at least ``nbytes`` long (None for 0)."""
     if nbytes == 0:
         return None
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_handle)
+    key = (_device_index(device), stream_handle)
+    capturing = torch.cuda.is_current_stream_capturing()
     with _ws_lock:
         ws = _workspaces.get(key)
-        if ws is not None and ws.numel() >= nbytes:
-            return ws
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError(
-                "w4a16: the split-K workspace must exist before HIP graph capture; run the "
-                "captured shapes once eagerly on the capture stream first (the reference's "
-                "graph capture also warms up before capturing, llama_paged_engine.py:315-347)"
-            )
-        size = max(nbytes, 1 << 20)
-        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        if ws is not None and ws.tensor.numel() >= nbytes:
+            if capturing:
+                ws.captured = True
+            elif not ws.defined:
+                ws.tensor.zero_()
+                ws.defined = True
+            return ws.tensor
+        size = max(nbytes, _MIN_WORKSPACE)
+        if ws is not None:
+            size = max(size, 2 * ws.tensor.numel())
+            if ws.captured:
+                _retired.append(ws.tensor)
+        ws = _Workspace(torch.zeros(size, dtype=torch.uint8, device=device), captured=capturing,
+                        defined=not capturing)
         _workspaces[key] = ws
-        return ws
+        return ws.tensor
+
+
+def reserve_workspace(nbytes: int, device=None, stream=None) -> None:
+    """Pre-size the workspace of ``stream`` (default: the current stream) to
+    ``nbytes``, e.g. with ``workspace_size`` of the largest call a graph will
+    capture.  Optional: without it the workspace grows on demand, in graph
+    captures too."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    s = torch.cuda.current_stream(dev) if stream is None else stream
+    with torch.cuda.device(dev), torch.cuda.stream(s):
+        get_workspace(dev, s.cuda_stream, nbytes)
+
+
+def workspace_status(device=None) -> int:
+    """OR of the status words of every live workspace (of ``device``, or all).
+
+    Synchronises the device.  A set W4A16_STATUS_SPLITK_TIMEOUT means a decode
+    finisher gave up and wrote NaN; the affected workspaces are zeroed here
+    (their slots may hold late partials) before the value is returned.
+    """
+    lib = load_library()
+    status = 0
+    with _ws_lock:
+        items = [(k, w) for k, w in _workspaces.items() if device is None or k[0] == _device_index(torch.device(device))]
+        for (dev, _), ws in items:
+            t = ws.tensor
+            off = ctypes.c_size_t(0)
+            if lib.w4a16_status_offset(t.numel(), ctypes.byref(off)) != W4A16_OK:
+                continue
+            with torch.cuda.device(dev):
+                torch.cuda.synchronize()
+                word = int(t[off.value:off.value + 4].cpu().view(torch.int32)[0])
+                if word:
+                    t.zero_()
+                    torch.cuda.synchronize()
+                    ws.defined = True
+            status |= word
+    return status
+
+
+def set_spin_limit(polls: int) -> int:
+    """Poll budget of the decode split-K finisher for later calls; returns the old one (tests only)."""
+    return int(load_library().w4a16_debug_set_spin_limit(polls))
 
 
 def linear(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_size: int) -> torch.Tensor:

@@ -12,6 +12,12 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SOURCES = [os.path.join(ROOT, "csrc", "w4a16_kernels.hip")]
+# Files the library is compiled from (sources and the headers they include).
+DEPENDENCIES = SOURCES + [
+    os.path.join(ROOT, "csrc", "w4a16_device.h"),
+    os.path.join(ROOT, "csrc", "slot_protocol.h"),
+    os.path.join(os.path.dirname(ROOT), "include", "w4a16.h"),
+]
 OUTPUT = os.path.join(HERE, "libw4a16.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -28,6 +34,14 @@ FLAGS = [
     # read and a write per element.
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
+
+
+def is_stale() -> bool:
+    """True when the library is missing or older than a file it is built from."""
+    if not os.path.exists(OUTPUT):
+        return True
+    built = os.path.getmtime(OUTPUT)
+    return any(os.path.exists(p) and os.path.getmtime(p) > built for p in DEPENDENCIES)
 
 
 def build(verbose: bool = False) -> str:

@@ -9,7 +9,10 @@ half (engine/kernels/quant.py:77-281):
 
 ``int4_matmul`` and device-tensor ``dequantize_weight_int4`` run the gfx950 HIP
 kernels of ``libw4a16.so`` through the C ABI; there is no Triton and no other
-backend.  ``int4_matmul`` refuses host tensors instead of computing on the CPU.
+device backend.  Host tensors keep the reference's host semantics
+(engine/kernels/quant.py:264-266): dequantize with the scales cast to the
+activation dtype, then ``a @ w`` in torch on the CPU.  A device tensor never
+takes that branch: if the library is missing, a device call raises.
 """
 
 from __future__ import annotations
@@ -94,13 +97,19 @@ def dequantize_weight_int4(packed: torch.Tensor, scale: torch.Tensor, group_size
         return _native.dequant(packed, scale.float(), group_size, scale.dtype)
 
 
+def _host_matmul(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_size: int) -> torch.Tensor:
+    """Host branch of int4_matmul (engine/kernels/quant.py:264-266): dense
+    weights in ``a.dtype`` (the scales are cast to it first), then ``a @ w``."""
+    if packed.is_cuda or scale.is_cuda:
+        raise ValueError("a, packed and scale must be on the same device")
+    w = dequantize_weight_int4(packed, scale.to(a.dtype), group_size)
+    return a @ w
+
+
 def _check_operands(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_size: int) -> torch.Tensor:
-    """Shape / dtype / device checks shared by int4_matmul and int4_matmul_grouped; returns fp32 scale."""
+    """Shape / dtype / device checks shared by the device entry points; returns fp32 scale."""
     if not a.is_cuda:
-        raise TypeError(
-            "w4a16.int4_matmul runs only on HIP device tensors; this package has no host "
-            "implementation of the fused contraction"
-        )
+        raise TypeError("the grouped and SwiGLU W4A16 entry points run on HIP device tensors only")
     assert group_size == FUSED_GROUP_SIZE, f"fused INT4 kernel requires group_size=128, got {group_size}"
     if a.dim() != 2 or packed.dim() != 2 or scale.dim() != 2:
         raise ValueError("int4_matmul expects a[M,K], packed[K/2,N], scale[K/128,N]")
@@ -145,20 +154,24 @@ def int4_matmul_grouped(a, weights, group_size: int = 128) -> list[torch.Tensor]
 def int4_matmul(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_size: int = 128) -> torch.Tensor:
     """Fused W4A16 matmul ``a @ dequantize(packed, scale)`` without a dense weight.
 
-    Drop-in for engine/kernels/quant.py:243-281.  ``a`` is ``(M, K)`` bf16 on a
-    HIP device, ``packed`` ``(K/2, N)`` int8, ``scale`` ``(K/128, N)`` float32.
-    Returns ``(M, N)`` bf16, allocated on the caller's stream; the call
-    enqueues on the current stream and never synchronises, so it can be
-    captured in a HIP graph once its workspace exists.
+    Drop-in for engine/kernels/quant.py:243-281.  On a HIP device ``a`` is
+    ``(M, K)`` bf16, ``packed`` ``(K/2, N)`` int8, ``scale`` ``(K/128, N)``
+    float32; the result is ``(M, N)`` bf16, allocated on the caller's stream.
+    The call enqueues on the current stream and never synchronises, so it can
+    be captured in a HIP graph (the split-K workspace is allocated inside the
+    capture if the capturing stream has none yet).  M <= 32 (M <= 64 on small
+    shapes) runs the HBM-bound decode kernel, larger M the MFMA GEMM.
 
-    M <= 32 (M <= 64 on small shapes) runs the HBM-bound decode kernel, larger M
-    the MFMA GEMM.
+    Host tensors take the reference's host branch (quant.py:264-266): any
+    float ``a``, result in ``a.dtype``, any group size.
 
     Raises:
-        AssertionError: ``group_size != 128`` (as engine/kernels/quant.py:267).
+        AssertionError: ``group_size != 128`` on a device (as engine/kernels/quant.py:267).
         ValueError: inconsistent shapes.
-        TypeError: host tensors or non-bf16 activations.
+        TypeError: non-bf16 device activations.
     """
+    if not a.is_cuda:
+        return _host_matmul(a, packed, scale, group_size)
     scale = _check_operands(a, packed, scale, group_size)
     with torch.cuda.device(a.device):
         return _native.linear(a, packed, scale, group_size)
@@ -170,9 +183,11 @@ def int4_swiglu(a: torch.Tensor, gate, up, group_size: int = 128) -> torch.Tenso
     ``gate`` and ``up`` are ``(packed, scale)`` pairs of the same shape.  The
     reference computes ``silu(linear(x, gate)) * linear(x, up)``
     (engine/llama_mlp.py:30-32, engine/llama_moe.py:44) as two int4_matmul
-    launches and two elementwise kernels; here decode-sized M is a single decode
-    launch with the epilogue on the fp32 sums, larger M the grouped GEMM plus
-    one elementwise pass.  Same checks and exceptions as ``int4_matmul``.
+    launches and two elementwise kernels.  Here decode-sized M is one decode
+    launch with the epilogue on the fp32 sums; GEMM-sized M is the row sums
+    plus one pair GEMM launch that stores ``silu(g) * u`` from the fp32 tiles
+    (operands it cannot take go through a grouped GEMM plus one elementwise
+    pass).  Device tensors only; same checks and exceptions as ``int4_matmul``.
     """
     (gp, gs), (up_p, us) = gate, up
     if gp.shape != up_p.shape or gs.shape != us.shape:

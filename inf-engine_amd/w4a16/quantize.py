@@ -166,10 +166,8 @@ def quantize_llama(model, group_size: int = 128):
             packed_bytes += w4.packed.numel() * w4.packed.element_size() + w4.scale.numel() * w4.scale.element_size()
 
     ratio = dense_bytes / max(packed_bytes, 1)
-    print(
-        f"Quantized {len(int4)} tensors across {config.n_layer} layers  "
-        f"({dense_bytes / 1e9:.2f} GB → {packed_bytes / 1e9:.2f} GB  {ratio:.1f}× reduction)"
-    )
+    print(f"w4a16: {len(int4)} projections of {config.n_layer} blocks now INT4, "
+          f"weights {dense_bytes / 1e9:.2f} -> {packed_bytes / 1e9:.2f} GB (x{ratio:.1f} smaller)")
     for key in int4:
         orig._t.pop(key, None)
     if torch.cuda.is_available():

@@ -27,7 +27,9 @@ How each function is pinned (tests/test_oracle.py):
   quantize         reference invariants (test_int4_quant.py:35-95: round-trip
                    error <= scale/2, lossless integer packing, ratio > 3.5),
                    round-half-to-even ties, amax -> +-7, and bit-exact agreement
-                   with an independent element-by-element Python restatement.
+                   with an independent element-by-element Python restatement
+                   (both division rules); the device rule itself is checked
+                   against torch on the GPU (tests/test_gpu_contract.py).
   dequantize       scale indexing with distinct power-of-two scales per
                    (group, column) and all-ones codes (any index slip is
                    bit-visible), and the golden fixture.
@@ -71,12 +73,21 @@ def codes(packed: np.ndarray) -> np.ndarray:
     return out
 
 
-def quantize(w: np.ndarray, group_size: int = 128) -> tuple[np.ndarray, np.ndarray]:
+def quantize(w: np.ndarray, group_size: int = 128, device_division: bool = False) -> tuple[np.ndarray, np.ndarray]:
     """Symmetric per-group INT4 quantization of w[d_in, d_out] (float32).
 
     Steps of quant.py:99-119: scale = max(amax_group|w| / 7, 1e-8) in float32;
     q = clip(round_half_even(w / scale), -7, 7); byte i = (q[2i] & 0xF) << 4 |
     (q[2i+1] & 0xF).
+
+    ``device_division``: the same op sequence as torch runs it on a GPU
+    tensor.  torch's device kernel for ``tensor / python_scalar`` multiplies by
+    the float32 reciprocal of the scalar instead of dividing (its true-division
+    kernel's CPU-scalar fast path), so the scale line ``amax / 7``
+    (quant.py:108) becomes ``amax * float32(1 / 7)``, which differs from the
+    quotient by one ulp for some amax.  ``w / scale`` (tensor by tensor) stays a
+    true division.  The reference quantizes on the GPU for models up to 8B
+    (main.py:474-478), so that is what its bytes are there.
     """
     w = np.asarray(w, dtype=np.float32)
     d_in, d_out = w.shape
@@ -86,7 +97,11 @@ def quantize(w: np.ndarray, group_size: int = 128) -> tuple[np.ndarray, np.ndarr
         raise ValueError(f"d_in={d_in} must be even for nibble packing")
     g = d_in // group_size
     wg = w.reshape(g, group_size, d_out)
-    scale = (np.abs(wg).max(axis=1) / np.float32(INT4_MAX)).astype(np.float32)
+    amax = np.abs(wg).max(axis=1)
+    if device_division:
+        scale = (amax * (np.float32(1.0) / np.float32(INT4_MAX))).astype(np.float32)
+    else:
+        scale = (amax / np.float32(INT4_MAX)).astype(np.float32)
     scale = np.maximum(scale, np.float32(1e-8))
     q = np.rint(wg / scale[:, None, :]).clip(-INT4_MAX, INT4_MAX).astype(np.int8).reshape(d_in, d_out)
     even = (q[0::2] & 0x0F).astype(np.uint8)

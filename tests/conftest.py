@@ -19,11 +19,10 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def native_lib():
-    """The ctypes handle of libw4a16.so, building it first only if it is absent."""
-    from w4a16 import _native
+    """The ctypes handle of libw4a16.so, (re)building it first when it is absent
+    or older than its sources (and hipcc is there to build it)."""
+    from w4a16 import _native, build
 
-    if not os.path.exists(_native.LIB_PATH):
-        from w4a16 import build
-
+    if build.is_stale() and (os.path.exists(build.HIPCC) or not os.path.exists(_native.LIB_PATH)):
         build.build()
     return _native.load_library()

@@ -3,11 +3,11 @@
 Bars (written out in each test):
 * unpack + scale indexing: bit-exact (dequant kernel; one-hot activations
   through the fused kernels; integer problems with power-of-two scales).
-* fused output: max |y - y_ref| <= 1e-2 * RMS(y_ref) + ulp_bf16(y_ref) / 2,
-  where y_ref is the float64 product of the same packed weights.  The half-ulp
-  term is the bf16 rounding of the output itself, which alone can exceed
-  1e-2 * RMS for |y| above ~2.5 RMS; a second, tighter bar (1e-3 * RMS on top of
-  the half ulp) catches real accumulation errors.
+* fused output: the one parity bar of oracle/tolerance.py,
+  max(|y - y_ref| - r * ulp_bf16(y_ref) / 2) <= 1e-3 * RMS(y_ref), where y_ref
+  is the float64 product of the same packed weights and r counts the bf16
+  roundings on the reference's path (1 everywhere except the GEMM-sized SwiGLU
+  fallback).
 Full benchmark shapes are checked against an fp32 torch dequantize-then-matmul
 of the same weights on the GPU plus a float64 oracle check on sampled columns.
 """
@@ -22,6 +22,7 @@ import pytest
 import torch
 
 from oracle import int4_oracle as orc
+from oracle.tolerance import assert_parity, ulp_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -41,21 +42,10 @@ def _gpu(native_lib):
     yield
 
 
-def ulp_bf16(v: np.ndarray) -> np.ndarray:
-    a = np.abs(v).astype(np.float64)
-    e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
-    return np.ldexp(1.0, (e - 7).astype(np.int64))
-
-
 def check_tolerance(y: torch.Tensor, y_ref: np.ndarray, label: str) -> None:
     yv = y.float().cpu().numpy().astype(np.float64)
-    rms = float(np.sqrt(np.mean(y_ref ** 2)))
-    err = np.abs(yv - y_ref)
-    excess = err - ulp_bf16(y_ref) / 2
-    say(f"  {label}: rms={rms:.4g} max|d|/rms={err.max() / rms:.3e} max(excess)/rms={excess.max() / rms:.3e}")
-    assert np.isfinite(yv).all(), label
-    assert excess.max() <= 1e-2 * rms, label
-    assert excess.max() <= 1e-3 * rms, label
+    rel = assert_parity(yv, y_ref, label)
+    say(f"  {label}: max(excess)/rms={rel:.3e}")
 
 
 def rand_problem(m, k, n, seed, dev=DEV):
@@ -550,6 +540,7 @@ def test_config4_qwen3_8b_prefill(name, k, n):
 
 @pytest.mark.parametrize("name,m,k,n", [("q", 1, 5120, 8192), ("kv", 1, 5120, 1024), ("o", 1, 8192, 5120),
                                         ("gate", 1, 5120, 25600), ("down", 1, 25600, 5120),
+                                        ("q", 4096, 5120, 8192), ("kv", 4096, 5120, 1024), ("o", 4096, 8192, 5120),
                                         ("gate", 4096, 5120, 25600), ("down", 4096, 25600, 5120)])
 def test_config5_qwen3_32b(name, m, k, n):
     full_size_check(m, k, n, seed=m + k + n, label=f"qwen3-32b {name} M={m}")
@@ -599,41 +590,31 @@ def test_lm_head_qwen3_8b_full_size():
     g = torch.Generator(device=DEV).manual_seed(5)
     w = (torch.randn(151936, 4096, generator=g, device=DEV) * 0.02).bfloat16()
     x = torch.randn(1, 4096, generator=g, device=DEV).bfloat16()
-    y = lm_head(x, w).float()
-    ref = (x.double() @ w.double().T).float()
-    rms = ref.pow(2).mean().sqrt()
-    _, e = torch.frexp(ref)  # |ref| = f * 2^e with f in [0.5, 1): a bf16 ulp is 2^(e - 8)
-    excess = (y - ref).abs() - torch.ldexp(torch.ones_like(ref), e - 9)
-    assert torch.isfinite(y).all()
-    assert excess.max().item() <= 1e-3 * rms.item()
+    y = lm_head(x, w)
+    ref = (x.double() @ w.double().T).cpu().numpy()
+    assert_parity(y.double().cpu().numpy(), ref, "lm_head full size")
     del w
 
 
 # ---------------------------------------------------------------------------
 # SwiGLU gate/up pair (w4a16_swiglu)
 #
-# Bar: max |h - h64| <= U * ulp_bf16(h64) + 1e-3 * RMS(h64), h64 the float64
-# oracle.  U = 1/2 for the fused forms (the decode pair, and the GEMM pair
-# kernel at GEMM-sized M): epilogue on the fp32 sums, one bf16 rounding.  The
-# fallback at GEMM-sized M (operands not aligned for the pair kernel) rounds
-# gate and up to bf16 before the epilogue, as the reference does
-# (engine/llama_mlp.py:30-32 rounds each linear output); the rounding of g
-# reaches h scaled by |g silu'(g) / silu(g)| <= 4 and the rounding of u by 1,
-# each at most 2^-9 relative, i.e. below ulp(h)/2 per unit, so U = 3.
+# Bar: oracle/tolerance.py against the float64 oracle h64, with r = 1 bf16
+# rounding for the fused forms (the decode pair, and the GEMM pair kernel at
+# GEMM-sized M: epilogue on the fp32 sums) and r = 6 for the fallback at
+# GEMM-sized M (operands not aligned for the pair kernel), which rounds gate
+# and up to bf16 before the epilogue as the reference does
+# (engine/llama_mlp.py:30-32 rounds each linear output).
 # ---------------------------------------------------------------------------
 
-def check_swiglu(h: torch.Tensor, h_ref: np.ndarray, m: int, label: str, units: float | None = None) -> None:
-    """max(|h - h_ref| - units * ulp_bf16(h_ref)) <= 1e-3 * RMS.  Fused forms (decode M, and the
-    GEMM pair kernel) round only h: half an ulp.  The grouped GEMM + elementwise form rounds gate
-    and up to bf16 first: 3 ulp."""
+def check_swiglu(h: torch.Tensor, h_ref: np.ndarray, m: int, label: str, roundings: int | None = None) -> None:
+    """The parity bar with r = 1 for the fused forms (decode M, and the GEMM pair kernel) and r = 6
+    for the grouped GEMM + elementwise form, which rounds gate and up to bf16 first."""
     hv = h.float().cpu().numpy().astype(np.float64)
-    rms = float(np.sqrt(np.mean(h_ref ** 2)))
-    if units is None:
-        units = 0.5 if m <= 32 else 3.0
-    excess = np.abs(hv - h_ref) - units * ulp_bf16(h_ref)
-    say(f"  {label}: rms={rms:.4g} max(excess)/rms={excess.max() / rms:.3e}")
-    assert np.isfinite(hv).all(), label
-    assert excess.max() <= 1e-3 * rms, label
+    if roundings is None:
+        roundings = 1 if m <= 32 else 6
+    rel = assert_parity(hv, h_ref, label, roundings)
+    say(f"  {label}: max(excess)/rms={rel:.3e}")
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 1024, 1536), (2, 128, 512), (5, 512, 1000), (16, 2048, 768),
@@ -681,12 +662,9 @@ def test_swiglu_qwen3_8b_full_size(m):
     h = int4_swiglu(x, gate, up)
     g, u = int4_matmul(x, *gate).double(), int4_matmul(x, *up).double()
     h_ref = (g * torch.sigmoid(g) * u).cpu().numpy()
-    # The reference-side g and u are themselves bf16-rounded: allow 3 ulp at every M.
-    hv = h.double().cpu().numpy()
-    rms = float(np.sqrt(np.mean(h_ref ** 2)))
-    excess = np.abs(hv - h_ref) - 3.0 * ulp_bf16(h_ref)
-    say(f"  vs two int4_matmul: max(excess)/rms={excess.max() / rms:.3e}")
-    assert excess.max() <= 1e-3 * rms
+    # The reference-side g and u are themselves bf16-rounded: r = 6 at every M.
+    rel = assert_parity(h.double().cpu().numpy(), h_ref, "vs two int4_matmul", roundings=6)
+    say(f"  vs two int4_matmul: max(excess)/rms={rel:.3e}")
     for _ in range(3):
         assert torch.equal(int4_swiglu(x, gate, up), h)
     # Sampled columns against the float64 oracle.  Every M here is a fused form (the decode pair,
@@ -694,7 +672,7 @@ def test_swiglu_qwen3_8b_full_size(m):
     cols = torch.randperm(n, generator=torch.Generator().manual_seed(m))[:48].sort().values.to(DEV)
     sub = [(p[:, cols].cpu().numpy(), s[:, cols].cpu().numpy()) for p, s in (gate, up)]
     check_swiglu(h[:, cols], orc.swiglu_reference(x.float().cpu().numpy(), *sub), m, "fp64 oracle, 48 cols",
-                 units=0.5)
+                 roundings=1)
 
 
 @pytest.mark.parametrize("m,odd_lds", [(2100, False), (2100, True), (2048, False)])
@@ -719,7 +697,7 @@ def test_swiglu_gemm_pair_kernel_and_fallback(m, odd_lds):
     sub = [(p[:, cols].cpu().numpy(), s[:, cols].contiguous().cpu().numpy()) for p, s in (gate, up)]
     ref = orc.swiglu_reference(x.float().cpu().numpy(), *sub)
     check_swiglu(h[:, cols], ref, m, f"M={m} {'fallback' if odd_lds else 'pair kernel'}",
-                 units=3.0 if odd_lds else 0.5)
+                 roundings=6 if odd_lds else 1)
 
 
 def test_swiglu_shares_workspace_and_edge_cases():
@@ -757,26 +735,29 @@ def test_swiglu_shares_workspace_and_edge_cases():
 
 
 def test_swiglu_mlp_layer_matches_unfused():
-    """swiglu_mlp with INT4 weights equals the reference composition
-    down(silu(gate(x)) * up(x)) to the bars above."""
-    from w4a16 import _Int4Weight, linear, swiglu_mlp, synth
+    """swiglu_mlp with INT4 weights is down(int4_swiglu(x)): h meets the bar
+    against the float64 oracle, the block output equals linear(h, down) bit
+    for bit, and that output meets the bar against the float64 product of h."""
+    from w4a16 import _Int4Weight, int4_swiglu, linear, swiglu_mlp, synth
 
     k, n = 512, 768
     ws = {}
     for name, (kk, nn), seed in (("gate", (k, n), 1), ("up", (k, n), 2), ("down", (n, k), 3)):
         p, s = synth.make_weight(kk, nn, seed=600 + seed, device=DEV)
         ws[f"mlp.{name}_proj.weight"] = _Int4Weight(p, s, 128, (nn, kk))
+    g_w, u_w, d_w = (ws[f"mlp.{p}_proj.weight"] for p in ("gate", "up", "down"))
     for m in (1, 48):
         x = synth.make_activations(2 * m, k, seed=610 + m, device=DEV).reshape(2, m, k)
         out = swiglu_mlp(x, ws)
         assert out.shape == (2, m, k)
-        g = linear(x, ws["mlp.gate_proj.weight"]).float()
-        u = linear(x, ws["mlp.up_proj.weight"]).float()
-        ref = linear((g * torch.sigmoid(g) * u).to(torch.bfloat16), ws["mlp.down_proj.weight"]).double()
-        rms = float(ref.pow(2).mean().sqrt())
-        err = float((out.double() - ref).abs().max())
-        say(f"  swiglu_mlp m={m}: max|d|/rms={err / rms:.3e}")
-        assert err <= 2e-2 * rms
+        xf = x.reshape(-1, k)
+        h = int4_swiglu(xf, (g_w.packed, g_w.scale), (u_w.packed, u_w.scale))
+        h64 = orc.swiglu_reference(xf.float().cpu().numpy(), (g_w.packed.cpu().numpy(), g_w.scale.cpu().numpy()),
+                                   (u_w.packed.cpu().numpy(), u_w.scale.cpu().numpy()))
+        check_swiglu(h, h64, 2 * m, f"swiglu_mlp h m={m}")
+        assert torch.equal(out.reshape(-1, k), linear(h, d_w))
+        y64 = orc.fused_reference(h.float().cpu().numpy(), d_w.packed.cpu().numpy(), d_w.scale.cpu().numpy())
+        check_tolerance(out.reshape(-1, k), y64, f"swiglu_mlp out m={m}")
 
 
 def test_qkv_projections_grouped_matches_linear():

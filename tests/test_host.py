@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(native_lib):
     assert set(names) == set(_native.EXPORTED_SYMBOLS), names
     for name in names:
         assert hasattr(native_lib, name), name
-    assert native_lib.w4a16_abi_version() == 5
+    assert native_lib.w4a16_abi_version() == _native.ABI_VERSION == 6
 
 
 def _linear(lib, *, x=1, ldx=4096, packed=1, ldp=4096, scale=1, lds=4096, y=1, ldy=4096, m=1, n=4096,
@@ -190,14 +190,51 @@ def test_swiglu_workspace_and_validation(native_lib):
     assert call(m=0, x=None, gp=None, gs=None, up=None, us=None, h=None) == nat.W4A16_OK
 
 
-def test_int4_matmul_rejects_host_tensors_and_bad_args():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("m,k,n,gs", [(1, 256, 64, 128), (4, 1024, 96, 128), (3, 512, 40, 64)])
+def test_int4_matmul_host_branch_matches_reference_cpu_path(dtype, m, k, n, gs):
+    """Host tensors: dequantize with scale.to(a.dtype), then a @ w
+    (engine/kernels/quant.py:264-266), bit-equal to the oracle's restatement."""
     from w4a16 import int4_matmul
+
+    g = torch.Generator().manual_seed(m + k + n)
+    packed = torch.randint(-128, 128, (k // 2, n), generator=g, dtype=torch.int8)
+    scale = torch.rand(k // gs, n, generator=g) * 0.01 + 1e-3
+    a = torch.randn(m, k, generator=g).to(dtype)
+    out = int4_matmul(a, packed, scale, gs)
+    assert out.dtype == dtype and out.shape == (m, n) and not out.is_cuda
+    assert torch.equal(out, orc.cpu_path(a, packed, scale, gs))
+
+
+def test_int4_matmul_host_close_to_fp():
+    """The reference's own invariant (tests/test_int4_quant.py:67-82) through
+    w4a16.int4_matmul on host tensors: relative error < 0.25."""
+    from w4a16 import int4_matmul, quantize_weight_int4
+
+    torch.manual_seed(2)
+    w = torch.randn(256, 128)
+    a = torch.randn(4, 256)
+    ref = a @ w
+    packed, scale = quantize_weight_int4(w, group_size=128)
+    out = int4_matmul(a, packed, scale, group_size=128)
+    rel_err = ((ref - out).norm() / ref.norm()).item()
+    assert rel_err < 0.25
+    # bf16 activations as the engine passes them
+    outb = int4_matmul(a.bfloat16(), packed, scale)
+    assert outb.dtype == torch.bfloat16
+    assert ((ref - outb.float()).norm() / ref.norm()).item() < 0.25
+
+
+def test_device_only_entry_points_reject_host_tensors():
+    from w4a16 import int4_matmul_grouped, int4_swiglu
 
     a = torch.randn(2, 256, dtype=torch.bfloat16)
     packed = torch.zeros(128, 64, dtype=torch.int8)
     scale = torch.ones(2, 64)
     with pytest.raises(TypeError):
-        int4_matmul(a, packed, scale)
+        int4_matmul_grouped(a, [(packed, scale)])
+    with pytest.raises(TypeError):
+        int4_swiglu(a, (packed, scale), (packed, scale))
 
 
 def test_quantize_matches_oracle_bit_exact():
@@ -298,8 +335,10 @@ def test_quantize_llama_structure_and_values():
     x = torch.randn(3, 64)
     wd = torch.randn(32, 64)
     assert torch.equal(linear(x, wd), x @ wd.T)
-    with pytest.raises(TypeError):
-        linear(torch.randn(1, 256, dtype=torch.bfloat16), q_model.w.layer(0)["self_attn.q_proj.weight"])
+    # On the host, INT4 weights take the reference's host branch (quant.py:264-266).
+    w4 = q_model.w.layer(0)["self_attn.q_proj.weight"]
+    xh = torch.randn(1, 256, dtype=torch.bfloat16)
+    assert torch.equal(linear(xh, w4), orc.cpu_path(xh, w4.packed, w4.scale))
 
 
 def test_quantized_to_device_requires_quantized_model():

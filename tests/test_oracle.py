@@ -87,16 +87,20 @@ def test_quantize_round_half_even_and_amax():
     assert np.all(np.abs(c).max(axis=0) == 7)
 
 
-def test_quantize_matches_elementwise_restatement():
-    """Bit-exact against an element-by-element restatement of quant.py:105-118."""
+@pytest.mark.parametrize("device_division", [False, True])
+def test_quantize_matches_elementwise_restatement(device_division):
+    """Bit-exact against an element-by-element restatement of quant.py:105-118
+    (host division, or torch's device rule amax * float32(1/7) for the scale)."""
     rng = np.random.default_rng(7)
     d_in, d_out, gs = 256, 24, 128
     w = (rng.standard_normal((d_in, d_out)) * 0.02).astype(np.float32)
-    packed, scale = orc.quantize(w, gs)
+    packed, scale = orc.quantize(w, gs, device_division=device_division)
+    inv7 = np.float32(1.0) / np.float32(7.0)
     for g in range(d_in // gs):
         for n in range(d_out):
             amax = np.float32(max(abs(float(v)) for v in w[g * gs:(g + 1) * gs, n]))
-            s = max(np.float32(amax / np.float32(7.0)), np.float32(1e-8))
+            q7 = np.float32(amax * inv7) if device_division else np.float32(amax / np.float32(7.0))
+            s = max(q7, np.float32(1e-8))
             assert scale[g, n] == s
             for r in range(gs):
                 k = g * gs + r
