@@ -114,6 +114,26 @@ int w4a16_linear(const void* x, int64_t ldx,
                  void* stream);
 
 /*
+ * w4a16_linear without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture with no allocator,
+ * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference.  Same arguments (minus the workspace), arithmetic, results
+ * and status codes as w4a16_linear.  Its scratch is a fixed 96 MiB array in
+ * the library's own device memory, one per GPU, held until the process ends;
+ * the first call on a device looks up its address and zeroes it on `stream`.
+ * Calls whose split-K scratch (w4a16_workspace_size) exceeds 96 MiB return
+ * W4A16_ERR_TOO_LARGE before anything is launched.  The call itself never
+ * allocates.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams or threads) race, so order them.
+ */
+int w4a16_linear_noalloc(const void* x, int64_t ldx,
+                         const int8_t* packed, int64_t ldp,
+                         const float* scale, int64_t lds,
+                         void* y, int64_t ldy,
+                         int M, int N, int K, int group_size,
+                         void* stream);
+
+/*
  * Several independent projections: up to W4A16_MAX_PROBLEMS problems, each
  * with its own M, activations, weights and output (problems may share x, e.g.
  * q/k/v or gate/up of a decoder block).  Problems that take the decode

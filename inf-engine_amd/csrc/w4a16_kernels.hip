@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "../../include/w4a16.h"
@@ -1837,6 +1838,52 @@ int check_all(const w4a16_problem* probs, int count, int group_size) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point (w4a16_linear_noalloc).
+//
+// One array per GPU in the library's own device memory, held until the
+// process ends.  It stands in for the caller's workspace: the lower half holds
+// the decode kernels' published-partial slots (zero between calls, like any
+// workspace), the upper half the GEMM's row sums and split partials, and the
+// last word the status word.  In host code `scratch` names a host-side shadow,
+// not device memory: the device address comes from hipGetSymbolAddress, once
+// per device with that device current, and only that pointer is ever passed
+// to a kernel.  Every call on a GPU shares its array, so calls that overlap on
+// one GPU (other streams, other threads) race.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = (size_t)96 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(u32x4_t* __restrict__ p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    p[i] = u32x4_t{0u, 0u, 0u, 0u};
+}
+
+// Device address of the current device's scratch; set up (address lookup and
+// a zero fill on `s`) on the first call on that device.
+int scratch_for_current_device(hipStream_t s, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return W4A16_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return W4A16_ERR_LAUNCH;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(1024), dim3(256), 0, s, static_cast<u32x4_t*>(p), kScratchBytes / 16);
+    if (hipGetLastError() != hipSuccess) return W4A16_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return W4A16_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
 extern "C" {
@@ -1902,6 +1949,24 @@ int w4a16_linear(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, 
   if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
   const w4a16_problem q{x, ldx, packed, ldp, scale, lds, y, ldy, M, N, K};
   return w4a16_linear_grouped(&q, 1, group_size, workspace, workspace_bytes, stream);
+}
+
+int w4a16_linear_noalloc(const void* x, int64_t ldx, const int8_t* packed, int64_t ldp, const float* scale,
+                         int64_t lds, void* y, int64_t ldy, int M, int N, int K, int group_size, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
+  const w4a16_problem q{x, ldx, packed, ldp, scale, lds, y, ldy, M, N, K};
+  int rc = check_all(&q, 1, group_size);
+  if (rc != W4A16_OK) return rc;
+  size_t need = 0;
+  rc = workspace_for(&q, 1, &need);
+  if (rc != W4A16_OK) return rc;
+  if (need > kScratchBytes) return W4A16_ERR_TOO_LARGE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (need == 0) return run(&q, 1, nullptr, 0, s);
+  void* ws = nullptr;
+  rc = scratch_for_current_device(s, &ws);
+  if (rc != W4A16_OK) return rc;
+  return run(&q, 1, ws, kScratchBytes, s);
 }
 
 int w4a16_workspace_size_swiglu(int M, int N, int K, int group_size, size_t* bytes) {

@@ -50,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "w4a16_workspace_size_swiglu",
     "w4a16_status_offset",
     "w4a16_debug_set_spin_limit",
+    "w4a16_linear_noalloc",
 )
 
 
@@ -105,6 +106,8 @@ def load_library() -> ctypes.CDLL:
         lib.w4a16_workspace_size.restype = i32
         lib.w4a16_linear.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp, sz, vp]
         lib.w4a16_linear.restype = i32
+        lib.w4a16_linear_noalloc.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
+        lib.w4a16_linear_noalloc.restype = i32
         lib.w4a16_dequant.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
         lib.w4a16_dequant.restype = i32
         lib.w4a16_swiglu.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64,
@@ -289,6 +292,22 @@ def linear(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_siz
     )
     check(rc, "w4a16_linear")
     return y
+
+
+def linear_noalloc(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, y: torch.Tensor,
+                   group_size: int = 128) -> None:
+    """y = a @ dequant(packed, scale) through w4a16_linear_noalloc, into the
+    caller's y (bf16 [M, N]); no workspace, no allocation in the call."""
+    lib = load_library()
+    m, k = a.shape
+    n = packed.shape[1]
+    a, ldx = _rows(a)
+    packed, ldp = _rows(packed)
+    scale, lds = _rows(scale)
+    stream = torch.cuda.current_stream(a.device).cuda_stream
+    rc = lib.w4a16_linear_noalloc(a.data_ptr(), ldx, packed.data_ptr(), ldp, scale.data_ptr(), lds,
+                                  y.data_ptr(), y.stride(0), m, n, k, group_size, stream)
+    check(rc, "w4a16_linear_noalloc")
 
 
 def linear_grouped(xs, weights, group_size: int) -> list[torch.Tensor]:

@@ -465,3 +465,19 @@ def test_gemm_copy_wait_walker_flags_short_paths():
                 "\ts_cbranch_scc1 .LBB0_1\n\ts_endpgm\n.Lfunc_end0:\n")
     assert _gemm_copy_wait_paths(fake(17), "fn") == []
     assert _gemm_copy_wait_paths(fake(16), "fn")
+
+
+def test_noalloc_entry_point_rejects_before_launch(native_lib):
+    """w4a16_linear_noalloc validates and sizes its scratch need on the host:
+    oversized, bad-group and null-pointer calls return codes without touching a GPU."""
+    from w4a16 import _native as nat
+
+    lib = native_lib
+    big = 1 << 40  # never dereferenced
+    assert lib.w4a16_linear_noalloc(big, 4096, big, 131072, big, 131072, big, 131072,
+                                    32, 131072, 4096, 128, None) == nat.W4A16_ERR_TOO_LARGE
+    assert lib.w4a16_linear_noalloc(big, 4096, big, 4096, big, 4096, big, 4096, 1, 4096, 4096, 64,
+                                    None) == nat.W4A16_ERR_GROUP_SIZE
+    assert lib.w4a16_linear_noalloc(None, 4096, big, 4096, big, 4096, big, 4096, 1, 4096, 4096, 128,
+                                    None) == nat.W4A16_ERR_NULL
+    assert lib.w4a16_linear_noalloc(None, 0, None, 0, None, 0, None, 0, 0, 16, 128, 128, None) == nat.W4A16_OK
