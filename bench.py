@@ -280,11 +280,15 @@ def roofline_prefill(us: float) -> dict:
     }
 
 
+KERNEL_SETS = ("gate_m1", "gate_m16", "gate_m32", "down_m32", "prefill_gate")
+
+
 def kernels_only(args) -> int:
-    """Only the roofline kernels (and optionally a copy of known size), for rocprofv3."""
+    """Only the roofline kernels (or the --kernels list), plus optionally a
+    copy of known size, for rocprofv3 (kernel traces and counter passes)."""
     import torch
 
-    from w4a16 import _native, synth
+    from w4a16 import _native, int4_matmul, synth
 
     _native.load_library()
     dev = torch.device("cuda:0")
@@ -300,17 +304,30 @@ def kernels_only(args) -> int:
         torch.cuda.synchronize()
         log(f"copy calibration: 3 x {src.numel() * 4} bytes read and written")
         del src, dst
-    gi = 4
-    weights = [[None] * 4 + [synth.make_weight(4096, 12288, seed=1000 * l + gi, device=dev)] for l in range(LAUNCHES)]
-    xs = {4096: synth.make_activations(1, 4096, seed=4096, device=dev)}
-    us = decode_gate_us(weights, xs, stream)
-    log(f"decode gate M=1: {us:.2f} us/launch")
-    out = {"decode_gate_m1": roofline_decode(us)}
-    if not args.no_prefill:
-        xp = {4096: synth.make_activations(2048, 4096, seed=4097, device=dev)}
-        us_p = prefill_gate_us(weights, xp, stream)
-        log(f"prefill gate M=2048: {us_p:.2f} us/launch")
-        out["prefill_gate_m2048"] = roofline_prefill(us_p)
+    which = args.kernels.split(",") if args.kernels else ["gate_m1"] + ([] if args.no_prefill else ["prefill_gate"])
+    for w in which:
+        if w not in KERNEL_SETS:
+            raise SystemExit(f"unknown kernel set {w!r}; choose from {KERNEL_SETS}")
+    gate = [synth.make_weight(4096, 12288, seed=1000 * l + 4, device=dev) for l in range(LAUNCHES)]
+    down = ([synth.make_weight(12288, 4096, seed=1000 * l + 6, device=dev) for l in range(LAUNCHES)]
+            if "down_m32" in which else None)
+    out = {}
+    for w in which:
+        if w == "prefill_gate":
+            x = synth.make_activations(2048, 4096, seed=4097, device=dev)
+            us = time_launches(lambda: [int4_matmul(x, *gate[l]) for l in range(LAUNCHES)], stream, reps=3)
+            out["prefill_gate_m2048"] = roofline_prefill(us)
+        else:
+            m = int(w.split("_m")[1])
+            k, ws = (12288, down) if w.startswith("down") else (4096, gate)
+            x = synth.make_activations(m, k, seed=k + m, device=dev)
+            us = time_launches(lambda: [int4_matmul(x, *ws[l]) for l in range(LAUNCHES)], stream)
+            n = ws[0][0].shape[1]
+            b = synth.algorithmic_bytes(m, k, n)
+            out[w] = {"us": round(us, 3), "GB/s": round(b / (us * 1e-6) / 1e9, 1)}
+            if w == "gate_m1":
+                out["decode_gate_m1"] = roofline_decode(us)
+        log(f"{w}: {us:.2f} us/launch")
     print(json.dumps(out), flush=True)
     return 0
 
@@ -327,6 +344,7 @@ def main() -> int:
     ap.add_argument("--no-32b", action="store_true", help="skip the Qwen3-32B (config 5) lines")
     ap.add_argument("--kernels-only", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--kernels", default="", help=f"--kernels-only: comma list of {KERNEL_SETS}")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
