@@ -230,20 +230,6 @@ def make_layers(layers: int, shapes, dev):
     ]
 
 
-def decode_gate_us(weights, xs, stream) -> float:
-    from w4a16 import int4_matmul
-
-    gi = 4  # gate_proj
-    return time_launches(lambda: [int4_matmul(xs[4096], *weights[l][gi]) for l in range(LAUNCHES)], stream)
-
-
-def prefill_gate_us(weights, xp, stream) -> float:
-    from w4a16 import int4_matmul
-
-    gi = 4
-    return time_launches(lambda: [int4_matmul(xp[4096], *weights[l][gi]) for l in range(LAUNCHES)], stream, reps=3)
-
-
 def roofline_decode(us: float) -> dict:
     from w4a16 import synth
 
