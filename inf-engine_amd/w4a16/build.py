@@ -21,12 +21,8 @@ DEPENDENCIES = SOURCES + [
 OUTPUT = os.path.join(HERE, "libw4a16.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-FLAGS = [
-    "--offload-arch=gfx950",
-    "-O3",
-    "-std=c++17",
-    "-fPIC",
-    "-shared",
+# Code-generation flags every compile of the kernel source uses.
+DEVICE_FLAGS = [
     # Keep the compiler from forming packed-fp32 VALU ops (v_pk_*_f32).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # MFMA accumulators in ordinary VGPRs: the kernels rescale their
@@ -34,6 +30,7 @@ FLAGS = [
     # read and a write per element.
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", *DEVICE_FLAGS]
 
 
 def is_stale() -> bool:
