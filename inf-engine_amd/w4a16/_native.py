@@ -238,28 +238,32 @@ def reserve_workspace(nbytes: int, device=None, stream=None) -> None:
 
 
 def workspace_status(device=None) -> int:
-    """OR of the status words of every live workspace (of ``device``, or all).
+    """OR of the status words of every workspace (of ``device``, or all),
+    the retired ones that captured graphs still use included.
 
     Synchronises the device.  A set W4A16_STATUS_SPLITK_TIMEOUT means a decode
     finisher gave up and wrote NaN; the affected workspaces are zeroed here
     (their slots may hold late partials) before the value is returned.
     """
     lib = load_library()
+    want = None if device is None else _device_index(torch.device(device))
     status = 0
     with _ws_lock:
-        items = [(k, w) for k, w in _workspaces.items() if device is None or k[0] == _device_index(torch.device(device))]
-        for (dev, _), ws in items:
-            t = ws.tensor
+        buffers = [(w.tensor, w) for w in _workspaces.values()] + [(t, None) for t in _retired]
+        for t, ws in buffers:
+            if want is not None and t.device.index != want:
+                continue
             off = ctypes.c_size_t(0)
             if lib.w4a16_status_offset(t.numel(), ctypes.byref(off)) != W4A16_OK:
                 continue
-            with torch.cuda.device(dev):
+            with torch.cuda.device(t.device):
                 torch.cuda.synchronize()
                 word = int(t[off.value:off.value + 4].cpu().view(torch.int32)[0])
                 if word:
                     t.zero_()
                     torch.cuda.synchronize()
-                    ws.defined = True
+                    if ws is not None:
+                        ws.defined = True
             status |= word
     return status
 
