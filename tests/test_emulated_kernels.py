@@ -1,0 +1,352 @@
+"""The gfx950 kernels run on the CPU under the wave emulator (tests/native/emu).
+
+inf-engine_amd/csrc/w4a16_kernels.hip is compiled as host C++ (three mechanical
+rewrites, tests/native/emu/prepare.py) and linked with a fiber-per-thread wave
+emulator; every entry point of the C ABI then runs the real kernel code on the
+CPU.  These tests check, with no GPU:
+
+* parity of every kernel family against the float64 oracle, at the bar of the
+  GPU tests (oracle/tolerance.py), on shapes across every planner branch and
+  the seeded random sweep of the GPU suite;
+* memory safety: every buffer handed to a kernel ends at an inaccessible page,
+  so a kernel that reads or writes past a buffer stops the run, and a negative
+  control shows that this detection works;
+* the workspace contract: the decode slot half is zero again after every call
+  and the status word stays clear;
+* determinism (two calls, identical bits).
+
+What the emulator does not model (timing, memory ordering between concurrent
+workgroups, late direct-to-LDS copies, the matrix cores' rounding order) is
+covered by the GPU suite only.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import shutil
+import subprocess
+import sys
+import textwrap
+
+import numpy as np
+import pytest
+
+from oracle import int4_oracle as orc
+from oracle.tolerance import assert_parity
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EMU = os.path.join(ROOT, "tests", "native", "emu")
+KERNELS = os.path.join(ROOT, "inf-engine_amd", "csrc", "w4a16_kernels.hip")
+
+
+def _clang() -> str | None:
+    for c in ("/opt/rocm/llvm/bin/clang++", shutil.which("clang++")):
+        if c and os.path.exists(c):
+            return c
+    return None
+
+
+def build_emulator(out_dir: str, source: str = KERNELS) -> str:
+    """Compile `source` with the wave emulator into out_dir/libw4a16_emu.so."""
+    sys.path.insert(0, EMU)
+    try:
+        import prepare
+    finally:
+        sys.path.remove(EMU)
+    tu = os.path.join(out_dir, "w4a16_host.cpp")
+    with open(source) as f:
+        text = prepare.transform(f.read())
+    with open(tu, "w") as f:
+        f.write(text)
+    lib = os.path.join(out_dir, "libw4a16_emu.so")
+    rt = os.path.join(out_dir, "emu_runtime.o")
+    inc = [f"-I{EMU}", f"-I{os.path.join(ROOT, 'inf-engine_amd', 'csrc')}", f"-I{os.path.join(ROOT, 'include')}"]
+    # The emulator (MFMA arithmetic, fiber switches) optimized; the kernel TU at
+    # -O0: it builds in seconds instead of a minute and runs about 1.5x slower.
+    for cmd in ([_clang(), "-O2", "-std=c++17", "-fPIC", "-c", *inc, os.path.join(EMU, "emu_runtime.cpp"), "-o", rt],
+                [_clang(), "-O0", "-g", "-std=c++17", "-shared", "-fPIC", *inc, tu, rt, "-o", lib]):
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        assert res.returncode == 0, res.stdout + res.stderr
+    return lib
+
+
+class Emu:
+    """ctypes view of the emulated library plus guarded host 'device' buffers."""
+
+    def __init__(self, path: str):
+        self.lib = lib = ctypes.CDLL(path)
+        vp, i64, i32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+        lib.emu_alloc.restype = vp
+        lib.emu_alloc.argtypes = [sz]
+        lib.w4a16_linear.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp, sz, vp]
+        lib.w4a16_linear_noalloc.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
+        lib.w4a16_workspace_size.argtypes = [i32, i32, i32, i32, ctypes.POINTER(sz)]
+        lib.w4a16_swiglu.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64,
+                                     i32, i32, i32, i32, vp, sz, vp]
+        lib.w4a16_workspace_size_swiglu.argtypes = [i32, i32, i32, i32, ctypes.POINTER(sz)]
+        lib.w4a16_bf16_gemv.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, vp]
+        lib.w4a16_dequant.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
+        lib.w4a16_status_offset.argtypes = [sz, ctypes.POINTER(sz)]
+        sys.path.insert(0, os.path.join(ROOT, "inf-engine_amd"))
+        from w4a16 import _native
+        self.Problem = _native.Problem
+        lib.w4a16_linear_grouped.argtypes = [ctypes.POINTER(_native.Problem), i32, i32, vp, sz, vp]
+        lib.w4a16_workspace_size_grouped.argtypes = [ctypes.POINTER(_native.Problem), i32, i32, ctypes.POINTER(sz)]
+
+    def put(self, arr: np.ndarray, extra: int = 0) -> int:
+        """Copy arr into a buffer that ends `extra` bytes after the array."""
+        a = np.ascontiguousarray(arr)
+        p = self.lib.emu_alloc(a.nbytes + extra)
+        ctypes.memmove(p, a.ctypes.data, a.nbytes)
+        return p
+
+    def zeros(self, nbytes: int) -> int:
+        p = self.lib.emu_alloc(nbytes)
+        ctypes.memset(p, 0, nbytes)
+        return p
+
+    def get(self, p: int, shape, dtype) -> np.ndarray:
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        return np.frombuffer(ctypes.string_at(p, n), dtype=dtype).reshape(shape).copy()
+
+    def workspace(self, nbytes: int) -> tuple[int | None, int]:
+        return (self.zeros(nbytes), nbytes) if nbytes else (None, 0)
+
+    def slots_clear(self, ws: int | None, nbytes: int) -> bool:
+        """Lower (slot) half zero and status word clear."""
+        if not ws:
+            return True
+        half = (nbytes // 2) & ~255
+        off = ctypes.c_size_t(0)
+        assert self.lib.w4a16_status_offset(nbytes, ctypes.byref(off)) == 0
+        low = self.get(ws, (half,), np.uint8)
+        status = self.get(ws + off.value, (1,), np.uint32)[0]
+        return not low.any() and status == 0
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_value(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.fixture(scope="module")
+def emu(tmp_path_factory):
+    if _clang() is None:
+        pytest.skip("clang++ not available")
+    return Emu(build_emulator(str(tmp_path_factory.mktemp("emu"))))
+
+
+def problem(m, k, n, seed, pad_x=0, pad_w=0, quantized=False):
+    """x (bf16 bits, [m, k + pad_x]), packed [k/2, n + pad_w], scale [k/128, n + pad_w]."""
+    rng = np.random.default_rng(seed)
+    if quantized:
+        w = (rng.standard_normal((k, n + pad_w)) * 0.02).astype(np.float32)
+        packed, scale = orc.quantize(w)
+    else:
+        packed = rng.integers(-128, 128, size=(k // 2, n + pad_w), dtype=np.int8)
+        scale = (rng.random((k // 128, n + pad_w), dtype=np.float32) * 0.01 + 0.001).astype(np.float32)
+    xb = bf16_bits(rng.standard_normal((m, k + pad_x)).astype(np.float32))
+    return xb, packed, scale
+
+
+def run_linear(emu, xb, packed, scale, m, k, n, misalign_x=False, check_ws=True):
+    lib = emu.lib
+    ldx, ldp, lds = xb.shape[1], packed.shape[1], scale.shape[1]
+    ws_bytes = ctypes.c_size_t(0)
+    assert lib.w4a16_workspace_size(m, n, k, 128, ctypes.byref(ws_bytes)) == 0
+    # Round the workspace to what _native would pass (it only grows), with slack.
+    nb = ws_bytes.value + (4096 if ws_bytes.value else 0)
+    ws, nb = emu.workspace(nb)
+    if misalign_x:
+        # One element off 16-byte alignment: the generic-load path.
+        base = emu.put(np.concatenate([np.zeros(1, np.uint16), xb.reshape(-1)]))
+        xp = base + 2
+    else:
+        xp = emu.put(xb)
+    y = emu.zeros(m * n * 2)
+    rc = lib.w4a16_linear(xp, ldx, emu.put(packed), ldp, emu.put(scale), lds, y, n, m, n, k, 128, ws, nb, None)
+    assert rc == 0, rc
+    if check_ws:
+        assert emu.slots_clear(ws, nb), "workspace slot half or status word not clear after the call"
+    return emu.get(y, (m, n), np.uint16)
+
+
+def reference(xb, packed, scale, m, k, n):
+    return orc.fused_reference(bf16_value(xb[:, :k]), packed[:, :n], scale[:, :n])
+
+
+# Shapes across the planner's branches: batch-1 decode, split / unsplit K,
+# 4 and 8 waves, 64- and 128-column strips, M subtiles (<= 16, <= 32, <= 64),
+# the GEMM (256- and 128-column tiles, two K halves, split K + reduce), odd N.
+SHAPES = [
+    (1, 128, 128), (1, 1024, 3072), (1, 4096, 1024), (1, 12288, 512), (2, 2048, 640), (4, 4096, 768),
+    (8, 1024, 256), (13, 512, 200), (16, 4096, 1024), (17, 1024, 512), (24, 2048, 384), (32, 4096, 2048),
+    (33, 512, 320), (48, 1024, 1000), (64, 2048, 512), (65, 512, 256), (100, 1024, 768),
+    (128, 4096, 1024), (200, 512, 2048), (256, 1024, 4096), (300, 1536, 333),
+]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+def test_linear_matches_oracle(emu, m, k, n):
+    xb, packed, scale = problem(m, k, n, seed=m * 7 + k + n, quantized=(m % 2 == 0))
+    y = run_linear(emu, xb, packed, scale, m, k, n)
+    assert_parity(bf16_value(y).astype(np.float64), reference(xb, packed, scale, m, k, n), f"emu M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("m", [1, 5, 24, 40, 130])
+def test_linear_strided_unaligned_and_sliced(emu, m):
+    """Row strides past K, activations off 16-byte alignment, column slices of
+    wider weight and scale tensors (the generic-load paths)."""
+    k, n = 1024, 300
+    xb, packed, scale = problem(m, k, n, seed=90 + m, pad_x=24, pad_w=100)
+    ref = reference(xb, packed, scale, m, k, n)
+    for misalign in (False, True):
+        # Slices: pass the wide tensors with the narrow n (row strides stay wide).
+        y = run_linear(emu, xb if not misalign else xb[:, :k], packed, scale, m, k, n, misalign_x=misalign)
+        assert_parity(bf16_value(y).astype(np.float64), ref, f"emu sliced M={m} misaligned={misalign}")
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 12288), (32, 12288, 1024), (2048, 512, 1024)])
+def test_linear_full_size_shapes(emu, m, k, n):
+    """Qwen3-8B gate at M = 1 (768 workgroups, 8-way split K), down's K at M = 32 (24 splits
+    in 8-wave workgroups), and a prefill-sized GEMM (16 row tiles)."""
+    xb, packed, scale = problem(m, k, n, seed=k + n, quantized=True)
+    y = run_linear(emu, xb, packed, scale, m, k, n)
+    assert_parity(bf16_value(y).astype(np.float64), reference(xb, packed, scale, m, k, n), f"emu M={m} K={k} N={n}")
+
+
+SWEEP_SEED = 20261202
+
+
+@pytest.mark.parametrize("case", range(32))
+def test_random_shape_sweep(emu, case):
+    """The GPU suite's seeded sweep (same shapes), on the emulator."""
+    rng = np.random.default_rng(SWEEP_SEED + case)
+    m = int(rng.choice([1, 2, 3, 5, 8, 13, 16, 17, 24, 31, 32, 33, 48, 64, 65, 96, 127, 128, 129, 200, 300]))
+    k = 128 * int(rng.integers(1, 17))
+    n = int(rng.integers(1, 2049))
+    pad_x = int(rng.choice([0, 0, 8, 24]))
+    pad_w = int(rng.choice([0, 0, 4, 100]))
+    xb, packed, scale = problem(m, k, n, seed=SWEEP_SEED + case, pad_x=pad_x, pad_w=pad_w)
+    y = run_linear(emu, xb, packed, scale, m, k, n)
+    assert_parity(bf16_value(y).astype(np.float64), reference(xb, packed, scale, m, k, n),
+                  f"emu sweep {case}: M={m} K={k} N={n} pad_x={pad_x} pad_w={pad_w}")
+
+
+def test_deterministic(emu):
+    xb, packed, scale = problem(4, 4096, 1024, seed=3)
+    a = run_linear(emu, xb, packed, scale, 4, 4096, 1024)
+    b = run_linear(emu, xb, packed, scale, 4, 4096, 1024)
+    assert np.array_equal(a, b)
+
+
+def test_grouped_matches_oracle(emu):
+    """q/k/v-like problems sharing x, plus experts with their own M, decode and GEMM sized."""
+    lib = emu.lib
+    specs = [(3, 1024, 512, 0), (3, 1024, 128, 0), (3, 1024, 128, 0), (7, 512, 384, 1), (96, 512, 256, 2)]
+    xs = {}
+    table = (emu.Problem * len(specs))()
+    outs, refs = [], []
+    for i, (m, k, n, xid) in enumerate(specs):
+        if xid not in xs:
+            xb, _, _ = problem(m, k, n, seed=500 + xid)
+            xs[xid] = (xb, emu.put(xb))
+        xb, xp = xs[xid]
+        _, packed, scale = problem(m, k, n, seed=600 + i, quantized=True)
+        y = emu.zeros(m * n * 2)
+        table[i] = emu.Problem(xp, k, emu.put(packed), n, emu.put(scale), n, y, n, m, n, k)
+        outs.append((y, m, n))
+        refs.append(reference(xb, packed, scale, m, k, n))
+    nb = ctypes.c_size_t(0)
+    assert lib.w4a16_workspace_size_grouped(table, len(specs), 128, ctypes.byref(nb)) == 0
+    ws, size = emu.workspace(nb.value)
+    assert lib.w4a16_linear_grouped(table, len(specs), 128, ws, size, None) == 0
+    assert emu.slots_clear(ws, size)
+    for (y, m, n), ref in zip(outs, refs):
+        assert_parity(bf16_value(emu.get(y, (m, n), np.uint16)).astype(np.float64), ref, f"emu grouped M={m} N={n}")
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1024, 1024), (5, 512, 384), (24, 1024, 256), (2048, 128, 2048), (256, 512, 1024), (130, 512, 200)])
+def test_swiglu_matches_oracle(emu, m, k, n):
+    """Decode pair kernel, the GEMM-sized pair kernel (256 tiles of 128 x 128: M=2048,
+    N=2048) and the grouped-GEMM + elementwise fallback (too few tiles, or odd N)."""
+    lib = emu.lib
+    xb, gp, gs = problem(m, k, n, seed=800 + m, quantized=True)
+    _, up, us = problem(m, k, n, seed=900 + m, quantized=True)
+    nb = ctypes.c_size_t(0)
+    assert lib.w4a16_workspace_size_swiglu(m, n, k, 128, ctypes.byref(nb)) == 0
+    ws, size = emu.workspace(nb.value)
+    h = emu.zeros(m * n * 2)
+    rc = lib.w4a16_swiglu(emu.put(xb), k, emu.put(gp), n, emu.put(gs), n, emu.put(up), n, emu.put(us), n,
+                          h, n, m, n, k, 128, ws, size, None)
+    assert rc == 0
+    xf = bf16_value(xb)
+    ref = orc.swiglu_reference(xf, (gp, gs), (up, us))
+    fallback = m > 64 and not (n % 128 == 0 and -(-m // 128) * (n // 128) >= 256)
+    assert_parity(bf16_value(emu.get(h, (m, n), np.uint16)).astype(np.float64), ref, f"emu swiglu M={m} N={n}",
+                  roundings=6 if fallback else 1)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1000, 4096), (3, 520, 1024), (4, 64, 640), (9, 200, 512), (16, 100, 1024)])
+def test_bf16_gemv_matches_oracle(emu, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    xb = bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    wb = bf16_bits((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    y = emu.zeros(m * n * 2)
+    assert emu.lib.w4a16_bf16_gemv(emu.put(xb), k, emu.put(wb), k, y, n, m, n, k, None) == 0
+    ref = bf16_value(xb).astype(np.float64) @ bf16_value(wb).astype(np.float64).T
+    assert_parity(bf16_value(emu.get(y, (m, n), np.uint16)).astype(np.float64), ref, f"emu gemv M={m} N={n} K={k}")
+
+
+def test_dequant_bit_exact(emu):
+    k, n = 512, 136
+    rng = np.random.default_rng(11)
+    packed = rng.integers(-128, 128, size=(k // 2, n), dtype=np.int8)
+    scale = np.ldexp(np.float32(1.0), rng.integers(-6, 6, size=(k // 128, n))).astype(np.float32)
+    pp, sp = emu.put(packed), emu.put(scale)
+    out = emu.zeros(k * n * 4)
+    assert emu.lib.w4a16_dequant(pp, n, sp, n, out, n, 0, k, n, 128, None) == 0
+    assert np.array_equal(emu.get(out, (k, n), np.float32), orc.dequantize(packed, scale))
+    out16 = emu.zeros(k * n * 2)
+    assert emu.lib.w4a16_dequant(pp, n, sp, n, out16, n, 1, k, n, 128, None) == 0
+    assert np.array_equal(emu.get(out16, (k, n), np.uint16), bf16_bits(orc.dequantize_bf16(packed, scale)))
+
+
+def test_noalloc_matches_linear(emu):
+    """The allocation-free entry point (its scratch is the emulated static array), two calls in a
+    row, the second smaller, against w4a16_linear."""
+    for m, k, n in ((4, 4096, 2048), (2, 1024, 512), (96, 512, 256)):
+        xb, packed, scale = problem(m, k, n, seed=m + 1)
+        ref = run_linear(emu, xb, packed, scale, m, k, n)
+        y = emu.zeros(m * n * 2)
+        rc = emu.lib.w4a16_linear_noalloc(emu.put(xb), k, emu.put(packed), n, emu.put(scale), n, y, n, m, n, k, 128, None)
+        assert rc == 0
+        assert np.array_equal(emu.get(y, (m, n), np.uint16), ref)
+
+
+def test_guard_pages_catch_an_out_of_bounds_kernel(tmp_path, emu):
+    """Negative control: an output buffer one row short makes the decode kernel's
+    last row store land on the guard page, and the emulator reports it."""
+    lib_path = emu.lib._name
+    script = textwrap.dedent(f"""
+        import ctypes, sys
+        sys.path[:0] = [{ROOT!r}, {os.path.join(ROOT, 'tests')!r}]
+        from test_emulated_kernels import Emu, problem
+        emu = Emu({lib_path!r})
+        m, k, n = 3, 512, 256
+        xb, packed, scale = problem(m, k, n, seed=1)
+        y = emu.zeros((m - 1) * n * 2)
+        nb = ctypes.c_size_t(0)
+        emu.lib.w4a16_workspace_size(m, n, k, 128, ctypes.byref(nb))
+        ws, size = emu.workspace(nb.value)
+        emu.lib.w4a16_linear(emu.put(xb), k, emu.put(packed), n, emu.put(scale), n, y, n, m, n, k, 128, ws, size, None)
+        print("no fault")
+    """)
+    res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 97, (res.returncode, res.stdout, res.stderr)
+    assert "memory access outside every buffer" in res.stderr and "gemv_kernel" in res.stderr, res.stderr
