@@ -37,7 +37,16 @@ struct Payload {
   int mask, width;
 };
 
+struct PendingCopy {
+  uint64_t issue;
+  char* dst;
+  char data[16];
+  int bytes;
+};
+
 struct Lane {
+  uint64_t vm_issued = 0;
+  std::vector<PendingCopy> pending;  // direct-to-LDS copies not yet landed
   void* sp = nullptr;
   char* stack = nullptr;
   emu_uint3 tid{0, 0, 0};
@@ -173,8 +182,21 @@ Payload& collective(int kind, const Payload& p) {
   return w.out[lane];
 }
 
+void land(Lane& L, uint64_t upto) {
+  size_t keep = 0;
+  for (size_t i = 0; i < L.pending.size(); ++i) {
+    PendingCopy& c = L.pending[i];
+    if (c.issue < upto)
+      memcpy(c.dst, c.data, c.bytes);
+    else
+      L.pending[keep++] = c;
+  }
+  L.pending.resize(keep);
+}
+
 void trampoline() {
   (*g_body)();
+  land(*g_cur, ~0ull);
   g_cur->done = true;
   --g_alive;
   Wave& w = g_waves[g_cur->tid.x / 64];
@@ -203,6 +225,8 @@ void init_lane(Lane& L) {
   L.done = false;
   L.wait_kind = 0;
   L.coll_seq = L.bar_seq = 0;
+  L.vm_issued = 0;
+  L.pending.clear();
 }
 
 bool ready(const Lane& L) {
@@ -285,6 +309,25 @@ float shfl_xor(float v, int mask, int width) {
   p.mask = mask;
   p.width = width;
   return collective(kShfl, p).f;
+}
+
+void vm_issue() { ++g_cur->vm_issued; }
+
+void vm_copy_to_lds(void* dst, const void* src, int bytes) {
+  PendingCopy c;
+  c.issue = g_cur->vm_issued++;
+  c.dst = static_cast<char*>(dst);
+  memcpy(c.data, src, bytes);
+  c.bytes = bytes;
+  g_cur->pending.push_back(c);
+}
+
+// s_waitcnt: the vmcnt field is bits 3:0 and 15:14 (6 bits); ops complete in
+// issue order, so all but the `n` youngest have landed after the wait.
+void waitcnt(int code) {
+  const uint64_t n = (uint64_t)((code & 15) | (((code >> 14) & 3) << 4));
+  Lane& L = *g_cur;
+  if (L.vm_issued >= n) land(L, L.vm_issued - n);
 }
 
 void syncthreads() {

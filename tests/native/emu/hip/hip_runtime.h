@@ -9,10 +9,11 @@
 // access past num_records reads zero / is dropped, per dword); every other
 // memory access is an ordinary host access, so a kernel that leaves its
 // buffers touches a guard page and is reported (emu_alloc in
-// emu_runtime.cpp).  What this does NOT model: memory ordering between
-// workgroups (they run one after another, in dispatch order), timing,
-// direct-to-LDS copies completing late, and the exact rounding order of the
-// matrix cores (the MFMA sums in fp32, k in order).
+// emu_runtime.cpp).  Direct-to-LDS copies land only when a wait
+// (s_waitcnt vmcnt) covers them, as on the hardware.  What this does NOT
+// model: memory ordering between workgroups (they run one after another, in
+// dispatch order), timing, and the exact rounding order of the matrix cores
+// (the MFMA sums in fp32, k in order).
 #pragma once
 
 #include <math.h>
@@ -79,6 +80,13 @@ float shfl_xor(float v, int mask, int width);
 void syncthreads();
 int lane_id();
 hipError_t last_error();
+// Vector-memory bookkeeping of the calling lane: every buffer access counts
+// as one operation in issue order; a direct-to-LDS copy reaches the LDS only
+// when a wait (s_waitcnt vmcnt(n)) leaves at most n younger operations
+// outstanding, as on the hardware, where such copies land asynchronously.
+void vm_issue();
+void vm_copy_to_lds(void* dst, const void* src, int bytes);
+void waitcnt(int code);
 
 inline emu_rsrc make_rsrc(const void* p, short, int num, int) { return emu_rsrc{static_cast<const char*>(p), (uint32_t)num}; }
 
@@ -87,6 +95,7 @@ inline emu_rsrc make_rsrc(const void* p, short, int num, int) { return emu_rsrc{
 // out-of-range stores are dropped.
 template <int BYTES>
 inline void buffer_load(emu_rsrc r, uint32_t voff, uint32_t soff, void* out) {
+  vm_issue();
   const uint64_t off = (uint64_t)voff + soff;
   const int unit = BYTES < 4 ? BYTES : 4;
   for (int i = 0; i < BYTES; i += unit) {
@@ -98,6 +107,7 @@ inline void buffer_load(emu_rsrc r, uint32_t voff, uint32_t soff, void* out) {
 }
 template <int BYTES>
 inline void buffer_store(emu_rsrc r, uint32_t voff, uint32_t soff, const void* in) {
+  vm_issue();
   const uint64_t off = (uint64_t)voff + soff;
   for (int i = 0; i < BYTES; i += 4)
     if (off + i + 4 <= r.num) memcpy(const_cast<char*>(r.base) + off + i, static_cast<const char*>(in) + i, 4);
@@ -108,13 +118,21 @@ inline uint32_t load_b32(emu_rsrc r, uint32_t v, uint32_t s, int) { uint32_t o; 
 inline uint16_t load_b16(emu_rsrc r, uint32_t v, uint32_t s, int) { uint16_t o; buffer_load<2>(r, v, s, &o); return o; }
 inline void store_b32(uint32_t x, emu_rsrc r, uint32_t v, uint32_t s, int) { buffer_store<4>(r, v, s, &x); }
 inline void store_b64(emu_u32x2 x, emu_rsrc r, uint32_t v, uint32_t s, int) { buffer_store<8>(r, v, s, &x); }
-// Direct-to-LDS load: lane l writes its `size` bytes at lds + offset + l * size.
+// Direct-to-LDS load: lane l's `size` bytes go to lds + offset + l * size once
+// a later wait covers the copy (vm_copy_to_lds).
 inline void load_lds(emu_rsrc r, void* lds, int size, uint32_t v, uint32_t s, int imm, int) {
   char* dst = static_cast<char*>(lds) + imm + lane_id() * size;
-  if (size == 16) buffer_load<16>(r, v + imm, s, dst);
-  else if (size == 4) buffer_load<4>(r, v + imm, s, dst);
-  else if (size == 2) buffer_load<2>(r, v + imm, s, dst);
-  else __builtin_trap();
+  char data[16];
+  const uint64_t off = (uint64_t)v + imm + s;
+  if (size != 16 && size != 4 && size != 2) __builtin_trap();
+  const int unit = size < 4 ? size : 4;
+  for (int i = 0; i < size; i += unit) {
+    if (off + i + unit <= r.num)
+      memcpy(data + i, r.base + off + i, unit);
+    else
+      memset(data + i, 0, unit);
+  }
+  vm_copy_to_lds(dst, data, size);
 }
 
 // v_perm_b32: bytes 0-3 of the pool are src1, 4-7 src0; selector bytes 8-11
@@ -180,7 +198,7 @@ inline T atomic_load(const T* p) { return *p; }
 #define __builtin_amdgcn_readfirstlane(v) ((int)emu::readfirstlane((uint32_t)(v)))
 #define __builtin_amdgcn_sched_barrier(m) ((void)0)
 #define __builtin_amdgcn_s_setprio(p) ((void)0)
-#define __builtin_amdgcn_s_waitcnt(c) ((void)0)
+#define __builtin_amdgcn_s_waitcnt(c) emu::waitcnt(c)
 
 #define __HIP_MEMORY_SCOPE_AGENT 3
 #define __hip_atomic_fetch_or(p, v, order, scope) emu::atomic_or((p), (v))

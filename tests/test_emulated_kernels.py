@@ -13,11 +13,12 @@ CPU.  These tests check, with no GPU:
   control shows that this detection works;
 * the workspace contract: the decode slot half is zero again after every call
   and the status word stays clear;
-* determinism (two calls, identical bits).
+* determinism (two calls, identical bits);
+* the GEMM's copy pipeline: direct-to-LDS copies land only at a wait that covers
+  them, so a wait one operation short reads stale tiles (negative control).
 
 What the emulator does not model (timing, memory ordering between concurrent
-workgroups, late direct-to-LDS copies, the matrix cores' rounding order) is
-covered by the GPU suite only.
+workgroups, the matrix cores' rounding order) is covered by the GPU suite only.
 """
 
 from __future__ import annotations
@@ -350,3 +351,22 @@ def test_guard_pages_catch_an_out_of_bounds_kernel(tmp_path, emu):
     res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=120)
     assert res.returncode == 97, (res.returncode, res.stdout, res.stderr)
     assert "memory access outside every buffer" in res.stderr and "gemv_kernel" in res.stderr, res.stderr
+
+
+def test_late_lds_copies_are_modelled(tmp_path):
+    """Negative control for the direct-to-LDS model: a GEMM whose copy wait leaves one
+    operation too many outstanding (vmcnt(18) instead of 17) reads activation tiles
+    before they land, and the emulated result is wrong."""
+    if _clang() is None:
+        pytest.skip("clang++ not available")
+    with open(KERNELS) as f:
+        src = f.read()
+    assert src.count("constexpr int kLoadsAfterA = 1 + 16;") == 1
+    bad = tmp_path / "w4a16_short_wait.hip"
+    bad.write_text(src.replace("constexpr int kLoadsAfterA = 1 + 16;", "constexpr int kLoadsAfterA = 1 + 17;"))
+    emu = Emu(build_emulator(str(tmp_path), str(bad)))
+    m, k, n = 256, 1024, 1024
+    xb, packed, scale = problem(m, k, n, seed=5)
+    y = run_linear(emu, xb, packed, scale, m, k, n)
+    with pytest.raises(AssertionError):
+        assert_parity(bf16_value(y).astype(np.float64), reference(xb, packed, scale, m, k, n), "short wait")
