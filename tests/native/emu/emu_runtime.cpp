@@ -75,6 +75,11 @@ char* g_lds = nullptr;
 size_t g_lds_map = 0;
 const char* g_kernel = "";
 hipError_t g_error = hipSuccess;
+// Order in which the scheduler visits a workgroup's threads each round:
+// 0 ascending, 1 descending, 2 a fresh pseudo-random permutation per round.
+// Results of a kernel without intra-workgroup races do not depend on it.
+int g_schedule = 0;
+uint64_t g_sched_state = 1;
 
 extern "C" void emu_ctx_switch(void** save_sp, void* new_sp);
 asm(R"(
@@ -379,10 +384,17 @@ void launch(const char* name, dim3 grid, dim3 block, size_t dyn, const std::func
         init_lane(g_lanes[t]);
         g_lanes[t].tid = emu_uint3{(unsigned)t, 0, 0};
       }
+      std::vector<int> order(nt);
+      for (int t = 0; t < nt; ++t) order[t] = g_schedule == 1 ? nt - 1 - t : t;
       while (g_alive > 0) {
         bool progressed = false;
-        for (int t = 0; t < nt; ++t) {
-          Lane& L = g_lanes[t];
+        if (g_schedule == 2)
+          for (int t = nt - 1; t > 0; --t) {
+            g_sched_state = g_sched_state * 6364136223846793005ull + 1442695040888963407ull;
+            std::swap(order[t], order[(g_sched_state >> 33) % (uint64_t)(t + 1)]);
+          }
+        for (int oi = 0; oi < nt; ++oi) {
+          Lane& L = g_lanes[order[oi]];
           if (!ready(L)) continue;
           L.wait_kind = 0;
           g_cur = &L;
@@ -398,6 +410,12 @@ void launch(const char* name, dim3 grid, dim3 block, size_t dyn, const std::func
 }
 
 }  // namespace emu
+
+// Scheduling order of the threads of a workgroup (see g_schedule).
+extern "C" void emu_set_schedule(int mode, uint64_t seed) {
+  g_schedule = mode;
+  g_sched_state = seed * 2 + 1;
+}
 
 // Test-side allocation of "device" buffers with guard pages.
 extern "C" void* emu_alloc(size_t bytes) {

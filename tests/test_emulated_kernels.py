@@ -15,7 +15,10 @@ CPU.  These tests check, with no GPU:
   and the status word stays clear;
 * determinism (two calls, identical bits);
 * the GEMM's copy pipeline: direct-to-LDS copies land only at a wait that covers
-  them, so a wait one operation short reads stale tiles (negative control).
+  them, so a wait one operation short reads stale tiles (negative control);
+* races inside a workgroup: results must not depend on the order in which the
+  emulator runs the threads between meeting points (a decode kernel with its
+  reduction barrier removed is the negative control).
 
 What the emulator does not model (timing, memory ordering between concurrent
 workgroups, the matrix cores' rounding order) is covered by the GPU suite only.
@@ -370,3 +373,51 @@ def test_late_lds_copies_are_modelled(tmp_path):
     y = run_linear(emu, xb, packed, scale, m, k, n)
     with pytest.raises(AssertionError):
         assert_parity(bf16_value(y).astype(np.float64), reference(xb, packed, scale, m, k, n), "short wait")
+
+
+def _set_schedule(emu, mode, seed=0):
+    emu.lib.emu_set_schedule.argtypes = [ctypes.c_int, ctypes.c_uint64]
+    emu.lib.emu_set_schedule(mode, seed)
+
+
+SCHEDULE_SHAPES = [(1, 1024, 512), (3, 4096, 1024), (16, 2048, 512), (24, 1024, 640), (40, 512, 320),
+                   (130, 512, 256), (256, 1024, 512), (200, 512, 333)]
+
+
+def test_results_do_not_depend_on_thread_schedule(emu):
+    """Race check inside workgroups: the emulator runs each workgroup's threads in
+    ascending, descending and two pseudo-random orders between meeting points.  A
+    read of LDS written by another thread without a barrier in between would see
+    different data under some order; every kernel must give identical bits."""
+    try:
+        for m, k, n in SCHEDULE_SHAPES:
+            xb, packed, scale = problem(m, k, n, seed=m)
+            outs = []
+            for i, mode in enumerate((0, 1, 2, 2)):
+                _set_schedule(emu, mode, 7 + i)
+                outs.append(run_linear(emu, xb, packed, scale, m, k, n))
+            for o in outs[1:]:
+                assert np.array_equal(outs[0], o), f"schedule-dependent result at M={m} K={k} N={n}"
+    finally:
+        _set_schedule(emu, 0)
+
+
+def test_schedule_check_finds_a_missing_barrier(tmp_path):
+    """Negative control: without the barrier between the decode kernel's LDS
+    stores of wave totals and their sum, the result depends on the schedule."""
+    if _clang() is None:
+        pytest.skip("clang++ not available")
+    with open(KERNELS) as f:
+        src = f.read()
+    barrier = "      }\n    }\n  __syncthreads();\n  const int elems = M * WCOLS;"
+    assert src.count(barrier) == 1
+    bad = tmp_path / "w4a16_no_barrier.hip"
+    bad.write_text(src.replace(barrier, "      }\n    }\n  const int elems = M * WCOLS;"))
+    emu = Emu(build_emulator(str(tmp_path), str(bad)))
+    m, k, n = 3, 4096, 1024
+    xb, packed, scale = problem(m, k, n, seed=m)
+    _set_schedule(emu, 0)
+    a = run_linear(emu, xb, packed, scale, m, k, n)
+    _set_schedule(emu, 1)
+    b = run_linear(emu, xb, packed, scale, m, k, n)
+    assert not np.array_equal(a, b)
