@@ -262,9 +262,11 @@ struct InstallHandler {
   }
 } g_install;
 
-// `bytes` of memory whose end abuts an inaccessible page (and whose first
-// page follows one), so reads or writes past the end fault.
-void* guarded(size_t bytes, size_t* mapped) {
+// `bytes` of memory between two inaccessible pages.  By default the buffer
+// ends where the trailing guard page begins, so reads or writes past the end
+// fault; with `front` it starts right after the leading guard page, so
+// accesses before the start fault.
+void* guarded(size_t bytes, size_t* mapped, bool front = false) {
   const size_t page = 4096;
   const size_t body = (bytes + page - 1) / page * page;
   const size_t total = body + 2 * page;
@@ -273,7 +275,7 @@ void* guarded(size_t bytes, size_t* mapped) {
   mprotect(m, page, PROT_NONE);
   mprotect(m + page + body, page, PROT_NONE);
   *mapped = total;
-  return m + page + body - bytes;
+  return front ? m + page : m + page + body - bytes;
 }
 
 }  // namespace
@@ -420,6 +422,11 @@ extern "C" void emu_set_schedule(int mode, uint64_t seed) {
 // Test-side allocation of "device" buffers with guard pages.
 extern "C" void* emu_alloc(size_t bytes) {
   size_t mapped = 0;
-  void* p = guarded(bytes == 0 ? 1 : bytes, &mapped);
-  return p;
+  return guarded(bytes == 0 ? 1 : bytes, &mapped);
+}
+
+// As emu_alloc, but the guard page precedes the buffer (catches underflow).
+extern "C" void* emu_alloc_front(size_t bytes) {
+  size_t mapped = 0;
+  return guarded(bytes == 0 ? 1 : bytes, &mapped, true);
 }

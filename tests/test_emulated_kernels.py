@@ -8,9 +8,11 @@ CPU.  These tests check, with no GPU:
 * parity of every kernel family against the float64 oracle, at the bar of the
   GPU tests (oracle/tolerance.py), on shapes across every planner branch and
   the seeded random sweep of the GPU suite;
-* memory safety: every buffer handed to a kernel ends at an inaccessible page,
-  so a kernel that reads or writes past a buffer stops the run, and a negative
-  control shows that this detection works;
+* memory safety: every buffer handed to a kernel ends at (or, for some cases,
+  starts right after) an inaccessible page, so a kernel that reads or writes
+  outside a buffer stops the run; operands off their natural alignment, row
+  strides past the row and buffers cut right after the last row are included,
+  and a negative control shows that the detection works;
 * the workspace contract: the decode slot half is zero again after every call
   and the status word stays clear;
 * determinism (two calls, identical bits);
@@ -421,3 +423,56 @@ def test_schedule_check_finds_a_missing_barrier(tmp_path):
     _set_schedule(emu, 1)
     b = run_linear(emu, xb, packed, scale, m, k, n)
     assert not np.array_equal(a, b)
+
+
+def _place(emu, arr, misalign: int, front: bool) -> int:
+    """Copy arr to a guarded buffer, `misalign` bytes after its start; the guard
+    page follows the data (front=False) or precedes the buffer (front=True)."""
+    a = np.ascontiguousarray(arr)
+    alloc = emu.lib.emu_alloc_front if front else emu.lib.emu_alloc
+    alloc.restype = ctypes.c_void_p
+    alloc.argtypes = [ctypes.c_size_t]
+    p = alloc(a.nbytes + misalign)
+    ctypes.memmove(p + misalign, a.ctypes.data, a.nbytes)
+    return p + misalign
+
+
+def _rows_with_stride(rows, cols, ld, dtype, fill):
+    """A [rows, ld] buffer cut right after the last row's `cols` elements."""
+    full = np.zeros((rows, ld), dtype=dtype)
+    full[:, :cols] = fill
+    return full.reshape(-1)[: (rows - 1) * ld + cols]
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_guarded_misaligned_operands(emu, case):
+    """Random shapes with operands off their natural alignment, row strides past the
+    row, buffers cut right after the last row, and the guard page before or after
+    every buffer: no kernel may touch a byte outside its operands."""
+    rng = np.random.default_rng(1000 + case)
+    m = int(rng.choice([1, 2, 3, 4, 7, 8, 12, 16, 17, 23, 32, 33, 40, 63, 64, 65, 100, 128, 129, 200, 257]))
+    k = 128 * int(rng.integers(1, 25))
+    n = int(rng.integers(1, 2200))
+    front = bool(rng.integers(0, 2))
+    ldx = k + int(rng.choice([0, 0, 1, 8, 13]))
+    ldp = n + int(rng.choice([0, 0, 1, 16, 33]))
+    lds = n + int(rng.choice([0, 0, 1, 4, 7]))
+    ldy = n + int(rng.choice([0, 0, 1, 4]))
+    mx, mp, ms, my = (int(rng.choice(c)) for c in ([0, 0, 2, 6, 8], [0, 0, 1, 4, 8, 12], [0, 0, 4, 8, 12], [0, 0, 2, 4, 6]))
+    packed = rng.integers(-128, 128, size=(k // 2, n), dtype=np.int8)
+    scale = (rng.random((k // 128, n), dtype=np.float32) * 0.01 + 0.001).astype(np.float32)
+    xb = bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    xp = _place(emu, _rows_with_stride(m, k, ldx, np.uint16, xb), mx, front)
+    pp = _place(emu, _rows_with_stride(k // 2, n, ldp, np.int8, packed), mp, front)
+    sp = _place(emu, _rows_with_stride(k // 128, n, lds, np.float32, scale), ms, front)
+    ylen = (m - 1) * ldy + n
+    yp = _place(emu, np.zeros(ylen, np.uint16), my, front)
+    nb = ctypes.c_size_t(0)
+    assert emu.lib.w4a16_workspace_size(m, n, k, 128, ctypes.byref(nb)) == 0
+    ws, size = emu.workspace(nb.value)
+    desc = f"M={m} K={k} N={n} ld={ldx},{ldp},{lds},{ldy} misalign={mx},{mp},{ms},{my} front={front}"
+    assert emu.lib.w4a16_linear(xp, ldx, pp, ldp, sp, lds, yp, ldy, m, n, k, 128, ws, size, None) == 0, desc
+    flat = np.frombuffer(ctypes.string_at(yp, ylen * 2), np.uint16)
+    y = np.stack([flat[r * ldy: r * ldy + n] for r in range(m)])
+    assert_parity(bf16_value(y).astype(np.float64), orc.fused_reference(bf16_value(xb), packed, scale), desc)
+    assert emu.slots_clear(ws, size), desc
