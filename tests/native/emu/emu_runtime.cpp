@@ -1,29 +1,40 @@
 // Wave emulator for running the gfx950 kernels on the CPU (tests only).
 //
-// A launch runs its workgroups one after another in dispatch order (x
-// fastest, then y).  Inside a workgroup every thread is a fiber with its own
-// stack; a fiber runs until it reaches a collective operation (MFMA, ballot,
-// readfirstlane, shuffle: the 64 lanes of its wave meet) or __syncthreads
-// (every live thread of the workgroup meets), then yields.  The last lane
-// to arrive computes the operation for the whole wave.  Lanes that return
-// leave the set a collective or barrier waits for, as exited waves do on the
-// hardware.  Lanes of one wave that reach different collectives, a barrier
-// that can never complete, or a kernel that touches memory outside its
-// buffers (guard pages around every emu_alloc buffer and the dynamic LDS)
-// stop the process with a message naming the kernel, workgroup and thread.
+// Every GPU thread is a fiber with its own stack.  A fiber runs until it
+// reaches a collective operation (MFMA, ballot, readfirstlane, shuffle: the
+// 64 lanes of its wave meet) or __syncthreads (every live thread of the
+// workgroup meets), then yields.  The last lane to arrive computes the
+// operation for the whole wave.  Lanes that return leave the set a
+// collective or barrier waits for, as exited waves do on the hardware.
+//
+// Workgroups are dispatched in order (x fastest, then y; or the reverse,
+// emu_set_dispatch) into a number of resident slots: one by default, so
+// workgroups run one after another, or more for the decode kernels
+// (emu_set_concurrency), whose resident workgroups then interleave at every
+// meeting point -- a split-K finisher polls while its publishers still run.
+// (The other kernels keep one slot: their static __shared__ arrays are
+// ordinary host statics, one copy for all workgroups.)
+//
+// Lanes of one wave that reach different collectives, a state in which no
+// live thread can move, or a kernel that touches memory outside its buffers
+// (guard pages around every emu_alloc buffer and the dynamic LDS) stop the
+// process with a message naming the kernel, workgroup and thread.
 #include <hip/hip_runtime.h>
 
 #include <signal.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 #include <sys/mman.h>
 #include <unistd.h>
 
+#include <algorithm>
+#include <deque>
 #include <vector>
 
 namespace {
 
-constexpr size_t kStackBytes = 256 * 1024;
+constexpr size_t kStackBytes = 128 * 1024;
 constexpr int kMaxThreads = 1024;
 constexpr size_t kMaxDynLds = 160 * 1024;
 
@@ -44,7 +55,10 @@ struct PendingCopy {
   int bytes;
 };
 
+struct Block;
+
 struct Lane {
+  Block* blk = nullptr;
   uint64_t vm_issued = 0;
   std::vector<PendingCopy> pending;  // direct-to-LDS copies not yet landed
   void* sp = nullptr;
@@ -64,15 +78,22 @@ struct Wave {
   bool present[64];
 };
 
-Lane g_lanes[kMaxThreads];
-Wave g_waves[kMaxThreads / 64];
-int g_nthreads = 0, g_alive = 0, g_bar_arrived = 0;
-uint64_t g_bar_seq = 0, g_bar_done = 0;
+struct Block {
+  emu_uint3 bid{0, 0, 0};
+  int nt = 0, alive = 0, bar_arrived = 0;
+  uint64_t bar_seq = 0, bar_done = 0;
+  std::vector<Lane*> lanes;
+  std::vector<int> order;
+  Wave waves[kMaxThreads / 64];
+  char* lds = nullptr;
+  char* lds_map = nullptr;
+  size_t lds_map_bytes = 0;
+};
+
+std::vector<Lane*> g_free_lanes;
 Lane* g_cur = nullptr;
 void* g_sched_sp = nullptr;
 const std::function<void()>* g_body = nullptr;
-char* g_lds = nullptr;
-size_t g_lds_map = 0;
 const char* g_kernel = "";
 hipError_t g_error = hipSuccess;
 // Order in which the scheduler visits a workgroup's threads each round:
@@ -80,6 +101,8 @@ hipError_t g_error = hipSuccess;
 // Results of a kernel without intra-workgroup races do not depend on it.
 int g_schedule = 0;
 uint64_t g_sched_state = 1;
+int g_concurrency = 1;     // resident workgroups of a decode-kernel launch
+bool g_reverse = false;    // dispatch the last workgroup first
 
 extern "C" void emu_ctx_switch(void** save_sp, void* new_sp);
 asm(R"(
@@ -106,8 +129,9 @@ emu_ctx_switch:
 )");
 
 [[noreturn]] void fail(const char* what) {
-  fprintf(stderr, "emu: %s in %s, workgroup (%u, %u), thread %u\n", what, g_kernel, emu::g_block_idx.x,
-          emu::g_block_idx.y, g_cur ? g_cur->tid.x : 0u);
+  const Block* b = g_cur ? g_cur->blk : nullptr;
+  fprintf(stderr, "emu: %s in %s, workgroup (%u, %u), thread %u\n", what, g_kernel, b ? b->bid.x : 0u,
+          b ? b->bid.y : 0u, g_cur ? g_cur->tid.x : 0u);
   fflush(stderr);
   _exit(97);
 }
@@ -118,7 +142,9 @@ void compute(Wave& w) {
   switch (w.kind) {
     case kMfma: {
       // D[m][n] = sum_k A[m][k] B[k][n] + C[m][n]; lane l holds A[l%16][8(l/16)+j],
-      // B[8(l/16)+j][l%16] and D[4(l/16)+r][l%16].
+      // B[8(l/16)+j][l%16] and D[4(l/16)+r][l%16].  The matrix cores read every lane.
+      for (int l = 0; l < 64; ++l)
+        if (!w.present[l]) fail("MFMA issued by a wave with exited lanes");
       float A[16][32], B[32][16], C[16][16];
       for (int l = 0; l < 64; ++l)
         for (int j = 0; j < 8; ++j) {
@@ -168,7 +194,7 @@ void compute(Wave& w) {
 Payload& collective(int kind, const Payload& p) {
   Lane* me = g_cur;
   const int lane = me->tid.x & 63;
-  Wave& w = g_waves[me->tid.x / 64];
+  Wave& w = me->blk->waves[me->tid.x / 64];
   const uint64_t seq = ++me->coll_seq;
   if (w.arrived == 0) {
     w.seq = seq;
@@ -201,21 +227,23 @@ void land(Lane& L, uint64_t upto) {
 
 void trampoline() {
   (*g_body)();
-  land(*g_cur, ~0ull);
-  g_cur->done = true;
-  --g_alive;
-  Wave& w = g_waves[g_cur->tid.x / 64];
+  Lane& me = *g_cur;
+  Block& b = *me.blk;
+  land(me, ~0ull);
+  me.done = true;
+  --b.alive;
+  Wave& w = b.waves[me.tid.x / 64];
   --w.alive;
   if (w.arrived > 0 && w.arrived == w.alive) compute(w);
-  if (g_bar_arrived > 0 && g_bar_arrived == g_alive) {
-    g_bar_done = g_bar_seq;
-    g_bar_arrived = 0;
+  if (b.bar_arrived > 0 && b.bar_arrived == b.alive) {
+    b.bar_done = b.bar_seq;
+    b.bar_arrived = 0;
   }
-  emu_ctx_switch(&g_cur->sp, g_sched_sp);
+  emu_ctx_switch(&me.sp, g_sched_sp);
   __builtin_trap();
 }
 
-// Fiber stack: return address of the first switch is the trampoline.
+// Fiber stack: the return address of the first switch is the trampoline.
 void init_lane(Lane& L) {
   if (!L.stack) {
     L.stack = static_cast<char*>(mmap(nullptr, kStackBytes, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS, -1, 0));
@@ -223,9 +251,9 @@ void init_lane(Lane& L) {
   }
   uintptr_t top = (reinterpret_cast<uintptr_t>(L.stack) + kStackBytes) & ~(uintptr_t)15;
   void** sp = reinterpret_cast<void**>(top);
-  *--sp = nullptr;                                  // alignment slot: trampoline entered with rsp % 16 == 8
-  *--sp = reinterpret_cast<void*>(&trampoline);     // ret target
-  for (int i = 0; i < 6; ++i) *--sp = nullptr;      // rbp rbx r12-r15
+  *--sp = nullptr;                               // alignment slot: trampoline entered with rsp % 16 == 8
+  *--sp = reinterpret_cast<void*>(&trampoline);  // ret target
+  for (int i = 0; i < 6; ++i) *--sp = nullptr;   // rbp rbx r12-r15
   L.sp = sp;
   L.done = false;
   L.wait_kind = 0;
@@ -236,8 +264,8 @@ void init_lane(Lane& L) {
 
 bool ready(const Lane& L) {
   if (L.done) return false;
-  if (L.wait_kind == 1) return g_waves[L.tid.x / 64].completed >= L.coll_seq;
-  if (L.wait_kind == 2) return g_bar_done >= L.bar_seq;
+  if (L.wait_kind == 1) return L.blk->waves[L.tid.x / 64].completed >= L.coll_seq;
+  if (L.wait_kind == 2) return L.blk->bar_done >= L.bar_seq;
   return true;
 }
 
@@ -266,7 +294,7 @@ struct InstallHandler {
 // ends where the trailing guard page begins, so reads or writes past the end
 // fault; with `front` it starts right after the leading guard page, so
 // accesses before the start fault.
-void* guarded(size_t bytes, size_t* mapped, bool front = false) {
+void* guarded(size_t bytes, size_t* mapped, char** base = nullptr, bool front = false) {
   const size_t page = 4096;
   const size_t body = (bytes + page - 1) / page * page;
   const size_t total = body + 2 * page;
@@ -275,18 +303,72 @@ void* guarded(size_t bytes, size_t* mapped, bool front = false) {
   mprotect(m, page, PROT_NONE);
   mprotect(m + page + body, page, PROT_NONE);
   *mapped = total;
+  if (base) *base = m;
   return front ? m + page : m + page + body - bytes;
+}
+
+Block* start_block(emu_uint3 bid, int nt, size_t dyn) {
+  Block* b = new Block();
+  b->bid = bid;
+  b->nt = b->alive = nt;
+  if (dyn > 0) {
+    b->lds = static_cast<char*>(guarded(dyn, &b->lds_map_bytes, &b->lds_map));
+    memset(b->lds, 0xA5, dyn);  // LDS starts undefined: make stale reads visible
+  }
+  for (int w = 0; w < (nt + 63) / 64; ++w) b->waves[w].alive = std::min(64, nt - 64 * w);
+  for (int t = 0; t < nt; ++t) {
+    Lane* L;
+    if (!g_free_lanes.empty()) {
+      L = g_free_lanes.back();
+      g_free_lanes.pop_back();
+    } else {
+      L = new Lane();
+    }
+    init_lane(*L);
+    L->tid = emu_uint3{(unsigned)t, 0, 0};
+    L->blk = b;
+    b->lanes.push_back(L);
+    b->order.push_back(g_schedule == 1 ? nt - 1 - t : t);
+  }
+  return b;
+}
+
+void finish_block(Block* b) {
+  for (Lane* L : b->lanes) g_free_lanes.push_back(L);
+  if (b->lds_map) munmap(b->lds_map, b->lds_map_bytes);
+  delete b;
+}
+
+// One round over a block's ready threads; returns whether any ran.
+bool run_round(Block& b) {
+  if (g_schedule == 2)
+    for (int t = b.nt - 1; t > 0; --t) {
+      g_sched_state = g_sched_state * 6364136223846793005ull + 1442695040888963407ull;
+      std::swap(b.order[t], b.order[(g_sched_state >> 33) % (uint64_t)(t + 1)]);
+    }
+  bool progressed = false;
+  for (int oi = 0; oi < b.nt; ++oi) {
+    Lane& L = *b.lanes[b.order[oi]];
+    if (!ready(L)) continue;
+    L.wait_kind = 0;
+    g_cur = &L;
+    emu_ctx_switch(&g_sched_sp, L.sp);
+    g_cur = nullptr;
+    progressed = true;
+  }
+  return progressed;
 }
 
 }  // namespace
 
 namespace emu {
 
-emu_uint3 g_block_idx{0, 0, 0}, g_grid_dim{1, 1, 1}, g_block_dim{1, 1, 1};
+emu_uint3 g_grid_dim{1, 1, 1}, g_block_dim{1, 1, 1};
 
 const emu_uint3* cur_tid() { return &g_cur->tid; }
+const emu_uint3* cur_bid() { return &g_cur->blk->bid; }
 int lane_id() { return g_cur->tid.x & 63; }
-void* dyn_lds() { return g_lds; }
+void* dyn_lds() { return g_cur->blk->lds; }
 hipError_t last_error() {
   const hipError_t e = g_error;
   g_error = hipSuccess;
@@ -339,12 +421,13 @@ void waitcnt(int code) {
 
 void syncthreads() {
   Lane* me = g_cur;
+  Block& b = *me->blk;
   const uint64_t seq = ++me->bar_seq;
-  if (g_bar_arrived == 0) g_bar_seq = seq;
-  else if (g_bar_seq != seq) fail("threads reached different barriers");
-  if (++g_bar_arrived == g_alive) {
-    g_bar_done = seq;
-    g_bar_arrived = 0;
+  if (b.bar_arrived == 0) b.bar_seq = seq;
+  else if (b.bar_seq != seq) fail("threads reached different barriers");
+  if (++b.bar_arrived == b.alive) {
+    b.bar_done = seq;
+    b.bar_arrived = 0;
   } else {
     me->wait_kind = 2;
     yield();
@@ -360,55 +443,38 @@ void launch(const char* name, dim3 grid, dim3 block, size_t dyn, const std::func
     g_error = hipErrorInvalidValue;
     return;
   }
-  size_t map = 0;
-  char* lds_map_base = nullptr;
-  if (dyn > 0) {
-    g_lds = static_cast<char*>(guarded(dyn, &map));
-    lds_map_base = g_lds + dyn - (map - 4096);  // start of the mapping
-  } else {
-    g_lds = nullptr;
-  }
   g_grid_dim = emu_uint3{grid.x, grid.y, 1};
   g_block_dim = emu_uint3{block.x, 1, 1};
   g_body = &body;
-  for (unsigned by = 0; by < grid.y; ++by)
-    for (unsigned bx = 0; bx < grid.x; ++bx) {
-      g_block_idx = emu_uint3{bx, by, 0};
-      if (g_lds) memset(g_lds, 0xA5, dyn);  // LDS starts undefined: make stale reads visible
-      g_nthreads = g_alive = nt;
-      g_bar_arrived = 0;
-      g_bar_seq = g_bar_done = 0;
-      for (int w = 0; w < (nt + 63) / 64; ++w) {
-        g_waves[w] = Wave{};
-        g_waves[w].alive = std::min(64, nt - 64 * w);
-      }
-      for (int t = 0; t < nt; ++t) {
-        init_lane(g_lanes[t]);
-        g_lanes[t].tid = emu_uint3{(unsigned)t, 0, 0};
-      }
-      std::vector<int> order(nt);
-      for (int t = 0; t < nt; ++t) order[t] = g_schedule == 1 ? nt - 1 - t : t;
-      while (g_alive > 0) {
-        bool progressed = false;
-        if (g_schedule == 2)
-          for (int t = nt - 1; t > 0; --t) {
-            g_sched_state = g_sched_state * 6364136223846793005ull + 1442695040888963407ull;
-            std::swap(order[t], order[(g_sched_state >> 33) % (uint64_t)(t + 1)]);
-          }
-        for (int oi = 0; oi < nt; ++oi) {
-          Lane& L = g_lanes[order[oi]];
-          if (!ready(L)) continue;
-          L.wait_kind = 0;
-          g_cur = &L;
-          emu_ctx_switch(&g_sched_sp, L.sp);
-          g_cur = nullptr;
-          progressed = true;
-        }
-        if (!progressed) fail("deadlock: every live thread waits at a collective or barrier that cannot complete");
+  const int slots = strstr(name, "gemv_kernel") ? std::max(1, g_concurrency) : 1;
+  const uint64_t nblocks = (uint64_t)grid.x * grid.y;
+  uint64_t next = 0;
+  std::deque<Block*> resident;
+  auto dispatch = [&]() {
+    while ((int)resident.size() < slots && next < nblocks) {
+      const uint64_t lin = g_reverse ? nblocks - 1 - next : next;
+      ++next;
+      resident.push_back(start_block(emu_uint3{(unsigned)(lin % grid.x), (unsigned)(lin / grid.x), 0}, nt, dyn));
+    }
+  };
+  dispatch();
+  while (!resident.empty()) {
+    bool progressed = false;
+    for (size_t i = 0; i < resident.size(); ++i) progressed |= run_round(*resident[i]);
+    for (size_t i = 0; i < resident.size();) {
+      if (resident[i]->alive == 0) {
+        finish_block(resident[i]);
+        resident.erase(resident.begin() + i);
+      } else {
+        ++i;
       }
     }
-  if (lds_map_base) munmap(lds_map_base, map);
-  g_lds = nullptr;
+    dispatch();
+    if (!progressed && !resident.empty()) {
+      g_cur = resident.front()->lanes.front();
+      fail("deadlock: every live thread waits at a collective or barrier that cannot complete");
+    }
+  }
 }
 
 }  // namespace emu
@@ -417,6 +483,13 @@ void launch(const char* name, dim3 grid, dim3 block, size_t dyn, const std::func
 extern "C" void emu_set_schedule(int mode, uint64_t seed) {
   g_schedule = mode;
   g_sched_state = seed * 2 + 1;
+}
+
+// Resident workgroups of decode-kernel launches (1: one after another), and
+// whether workgroups are dispatched last-first.
+extern "C" void emu_set_concurrency(int slots, int reverse) {
+  g_concurrency = slots;
+  g_reverse = reverse != 0;
 }
 
 // Test-side allocation of "device" buffers with guard pages.
@@ -428,5 +501,5 @@ extern "C" void* emu_alloc(size_t bytes) {
 // As emu_alloc, but the guard page precedes the buffer (catches underflow).
 extern "C" void* emu_alloc_front(size_t bytes) {
   size_t mapped = 0;
-  return guarded(bytes == 0 ? 1 : bytes, &mapped, true);
+  return guarded(bytes == 0 ? 1 : bytes, &mapped, nullptr, true);
 }

@@ -10,10 +10,12 @@
 // memory access is an ordinary host access, so a kernel that leaves its
 // buffers touches a guard page and is reported (emu_alloc in
 // emu_runtime.cpp).  Direct-to-LDS copies land only when a wait
-// (s_waitcnt vmcnt) covers them, as on the hardware.  What this does NOT
-// model: memory ordering between workgroups (they run one after another, in
-// dispatch order), timing, and the exact rounding order of the matrix cores
-// (the MFMA sums in fp32, k in order).
+// (s_waitcnt vmcnt) covers them, as on the hardware.  Workgroups run one
+// after another in dispatch order, or (decode kernels, emu_set_concurrency)
+// several at once, interleaved at every meeting point.  What this does NOT
+// model: timing, caches and the memory ordering they allow (every store is
+// visible to every later load at once), and the exact rounding order of the
+// matrix cores (the MFMA sums in fp32, k in order).
 #pragma once
 
 #include <math.h>
@@ -70,7 +72,8 @@ namespace emu {
 
 // Launch, lane and collective services (emu_runtime.cpp).
 const emu_uint3* cur_tid();
-extern emu_uint3 g_block_idx, g_grid_dim, g_block_dim;
+const emu_uint3* cur_bid();
+extern emu_uint3 g_grid_dim, g_block_dim;
 void launch(const char* name, dim3 grid, dim3 block, size_t dyn_lds, const std::function<void()>& body);
 void* dyn_lds();
 emu_f32x4 mfma_16x16x32_bf16(emu_bf16x8 a, emu_bf16x8 b, emu_f32x4 c);
@@ -172,7 +175,7 @@ inline T atomic_load(const T* p) { return *p; }
 }  // namespace emu
 
 #define threadIdx (*emu::cur_tid())
-#define blockIdx (emu::g_block_idx)
+#define blockIdx (*emu::cur_bid())
 #define gridDim (emu::g_grid_dim)
 #define blockDim (emu::g_block_dim)
 

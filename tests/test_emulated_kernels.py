@@ -20,10 +20,15 @@ CPU.  These tests check, with no GPU:
   them, so a wait one operation short reads stale tiles (negative control);
 * races inside a workgroup: results must not depend on the order in which the
   emulator runs the threads between meeting points (a decode kernel with its
-  reduction barrier removed is the negative control).
+  reduction barrier removed is the negative control);
+* the decode split-K protocol with every workgroup resident and interleaved,
+  dispatched first-to-last and last-to-first (finishers then poll while their
+  publishers run): identical bits, empty slots; and its give-up path, forced
+  with a zero poll budget and finishers dispatched before their publishers.
 
-What the emulator does not model (timing, memory ordering between concurrent
-workgroups, the matrix cores' rounding order) is covered by the GPU suite only.
+What the emulator does not model (timing, caches and the store-to-load
+ordering they allow between workgroups, the matrix cores' rounding order) is
+covered by the GPU suite only.
 """
 
 from __future__ import annotations
@@ -476,3 +481,84 @@ def test_guarded_misaligned_operands(emu, case):
     y = np.stack([flat[r * ldy: r * ldy + n] for r in range(m)])
     assert_parity(bf16_value(y).astype(np.float64), orc.fused_reference(bf16_value(xb), packed, scale), desc)
     assert emu.slots_clear(ws, size), desc
+
+
+def _set_concurrency(emu, slots, reverse=False):
+    emu.lib.emu_set_concurrency.argtypes = [ctypes.c_int, ctypes.c_int]
+    emu.lib.emu_set_concurrency(slots, 1 if reverse else 0)
+
+
+# Decode launches with split K: (M, K, N) -> workgroups (strips x splits).
+SPLIT_K_SHAPES = [(1, 4096, 512), (1, 12288, 256), (4, 4096, 384), (16, 2048, 512), (24, 2048, 640), (40, 1024, 256)]
+
+
+@pytest.mark.parametrize("reverse", [False, True])
+def test_split_k_with_resident_workgroups(emu, reverse):
+    """Every workgroup of a decode launch resident at once and interleaved at each
+    meeting point, dispatched first-to-last or last-to-first: split-K finishers
+    poll while their publishers still run.  Results must equal the one-at-a-time
+    run bit for bit (partials are summed in split order, not arrival order), and
+    the slots must be empty again."""
+    try:
+        for m, k, n in SPLIT_K_SHAPES:
+            xb, packed, scale = problem(m, k, n, seed=m + k + n, quantized=True)
+            _set_concurrency(emu, 1)
+            seq = run_linear(emu, xb, packed, scale, m, k, n)
+            _set_concurrency(emu, 4096, reverse)
+            conc = run_linear(emu, xb, packed, scale, m, k, n)
+            assert np.array_equal(seq, conc), f"M={m} K={k} N={n} reverse={reverse}"
+        # The SwiGLU pair: every gate workgroup publishes, up's finishers sum both.
+        m, k, n = 3, 2048, 512
+        xb, gp, gs = problem(m, k, n, seed=71, quantized=True)
+        _, up, us = problem(m, k, n, seed=72, quantized=True)
+        nb = ctypes.c_size_t(0)
+        assert emu.lib.w4a16_workspace_size_swiglu(m, n, k, 128, ctypes.byref(nb)) == 0
+        outs = []
+        for slots in (1, 4096):
+            _set_concurrency(emu, slots, reverse and slots > 1)
+            ws, size = emu.workspace(nb.value)
+            h = emu.zeros(m * n * 2)
+            assert emu.lib.w4a16_swiglu(emu.put(xb), k, emu.put(gp), n, emu.put(gs), n, emu.put(up), n,
+                                        emu.put(us), n, h, n, m, n, k, 128, ws, size, None) == 0
+            assert emu.slots_clear(ws, size)
+            outs.append(emu.get(h, (m, n), np.uint16))
+        assert np.array_equal(outs[0], outs[1])
+    finally:
+        _set_concurrency(emu, 1)
+
+
+def test_split_k_give_up_path(emu):
+    """The finisher's bounded poll, forced: finishers dispatched before their
+    publishers (last-first, one at a time) with a zero poll budget give up.  Their
+    outputs are NaN, the status word says so, the late publishers leave their
+    slots set (the workspace must be zeroed before reuse), and every kernel ends.
+    A zeroed workspace then gives exact results again."""
+    lib = emu.lib
+    lib.w4a16_debug_set_spin_limit.argtypes = [ctypes.c_uint32]
+    lib.w4a16_debug_set_spin_limit.restype = ctypes.c_uint32
+    m, k, n = 1, 4096, 512
+    xb, packed, scale = problem(m, k, n, seed=5, quantized=True)
+    ref = run_linear(emu, xb, packed, scale, m, k, n)
+    nb = ctypes.c_size_t(0)
+    assert lib.w4a16_workspace_size(m, n, k, 128, ctypes.byref(nb)) == 0
+    ws, size = emu.workspace(nb.value)
+    xp, pp, sp = emu.put(xb), emu.put(packed), emu.put(scale)
+    old = lib.w4a16_debug_set_spin_limit(0)
+    try:
+        _set_concurrency(emu, 1, reverse=True)
+        y = emu.zeros(m * n * 2)
+        assert lib.w4a16_linear(xp, k, pp, n, sp, n, y, n, m, n, k, 128, ws, size, None) == 0
+    finally:
+        lib.w4a16_debug_set_spin_limit(old)
+        _set_concurrency(emu, 1)
+    out = emu.get(y, (m, n), np.uint16)
+    assert (out == 0x7FC0).all()  # every strip's finisher ran before its publishers
+    off = ctypes.c_size_t(0)
+    assert lib.w4a16_status_offset(size, ctypes.byref(off)) == 0
+    assert emu.get(ws + off.value, (1,), np.uint32)[0] & 1  # W4A16_STATUS_SPLITK_TIMEOUT
+    assert not emu.slots_clear(ws, size)
+    ctypes.memset(ws, 0, size)
+    y2 = emu.zeros(m * n * 2)
+    assert lib.w4a16_linear(xp, k, pp, n, sp, n, y2, n, m, n, k, 128, ws, size, None) == 0
+    assert np.array_equal(emu.get(y2, (m, n), np.uint16), ref)
+    assert emu.slots_clear(ws, size)
