@@ -7,11 +7,11 @@
 // operation for the whole wave.  Lanes that return leave the set a
 // collective or barrier waits for, as exited waves do on the hardware.
 //
-// Workgroups are dispatched in order (x fastest, then y; or the reverse,
-// emu_set_dispatch) into a number of resident slots: one by default, so
-// workgroups run one after another, or more for the decode kernels
-// (emu_set_concurrency), whose resident workgroups then interleave at every
-// meeting point -- a split-K finisher polls while its publishers still run.
+// Workgroups are dispatched in order (x fastest, then y; or the reverse) into
+// a number of resident slots (both set by emu_set_concurrency): one by
+// default, so workgroups run one after another, or more for the decode
+// kernels, whose resident workgroups then interleave at every meeting point
+// -- a split-K finisher polls while its publishers still run.
 // (The other kernels keep one slot: their static __shared__ arrays are
 // ordinary host statics, one copy for all workgroups.)
 //
@@ -492,14 +492,27 @@ extern "C" void emu_set_concurrency(int slots, int reverse) {
   g_reverse = reverse != 0;
 }
 
-// Test-side allocation of "device" buffers with guard pages.
-extern "C" void* emu_alloc(size_t bytes) {
+// Test-side allocation of "device" buffers with guard pages; every mapping
+// is recorded so that emu_free_all can release them between tests.
+namespace {
+std::vector<std::pair<char*, size_t>> g_buffers;
+
+void* test_buffer(size_t bytes, bool front) {
   size_t mapped = 0;
-  return guarded(bytes == 0 ? 1 : bytes, &mapped);
+  char* base = nullptr;
+  void* p = guarded(bytes == 0 ? 1 : bytes, &mapped, &base, front);
+  if (p) g_buffers.emplace_back(base, mapped);
+  return p;
 }
+}  // namespace
+
+extern "C" void* emu_alloc(size_t bytes) { return test_buffer(bytes, false); }
 
 // As emu_alloc, but the guard page precedes the buffer (catches underflow).
-extern "C" void* emu_alloc_front(size_t bytes) {
-  size_t mapped = 0;
-  return guarded(bytes == 0 ? 1 : bytes, &mapped, nullptr, true);
+extern "C" void* emu_alloc_front(size_t bytes) { return test_buffer(bytes, true); }
+
+// Unmap every buffer emu_alloc / emu_alloc_front returned.
+extern "C" void emu_free_all() {
+  for (auto& b : g_buffers) munmap(b.first, b.second);
+  g_buffers.clear();
 }

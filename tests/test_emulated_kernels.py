@@ -152,6 +152,14 @@ def emu(tmp_path_factory):
     return Emu(build_emulator(str(tmp_path_factory.mktemp("emu"))))
 
 
+@pytest.fixture(autouse=True)
+def _release_buffers(request):
+    """Unmap the guarded buffers a test allocated (the library stays loaded)."""
+    yield
+    if "emu" in request.fixturenames:
+        request.getfixturevalue("emu").lib.emu_free_all()
+
+
 def problem(m, k, n, seed, pad_x=0, pad_w=0, quantized=False):
     """x (bf16 bits, [m, k + pad_x]), packed [k/2, n + pad_w], scale [k/128, n + pad_w]."""
     rng = np.random.default_rng(seed)
