@@ -171,9 +171,13 @@ void compute(Wave& w) {
       break;
     }
     case kFirst: {
+      // The kernels use readfirstlane to move a wave-uniform value into a
+      // scalar register; a value that differs between lanes is a bug there.
       int first = -1;
       for (int l = 0; l < 64 && first < 0; ++l)
         if (w.present[l]) first = l;
+      for (int l = 0; l < 64; ++l)
+        if (w.present[l] && w.in[l].u != w.in[first].u) fail("readfirstlane of a value that differs between lanes");
       for (int l = 0; l < 64; ++l) w.out[l].u = w.in[first].u;
       break;
     }
