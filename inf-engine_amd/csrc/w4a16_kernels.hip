@@ -1256,9 +1256,9 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
   if (idx >= total) return;
   const int i = (int)(idx / N);
   const int n = (int)(idx % N);
-  const int8_t byte = (int8_t)packed[(int64_t)i * ldp + n];
-  const int q_even = byte >> 4;  // arithmetic shift: [-8, 7]
-  const int q_odd = (int)(int8_t)(uint8_t)(byte << 4) >> 4;
+  const uint8_t byte = packed[(int64_t)i * ldp + n];
+  const int q_even = (int8_t)byte >> 4;                  // arithmetic shift: [-8, 7]
+  const int q_odd = (int8_t)(uint8_t)(byte << 4) >> 4;   // low nibble moved up, shifted back
   const int k = 2 * i;
   float s = scale[(int64_t)(k / group_size) * lds + n];
   if (out_bf16) {

@@ -58,8 +58,17 @@ def _clang() -> str | None:
     return None
 
 
-def build_emulator(out_dir: str, source: str = KERNELS) -> str:
-    """Compile `source` with the wave emulator into out_dir/libw4a16_emu.so."""
+def _ubsan_runtime() -> str | None:
+    import glob
+    libs = glob.glob(os.path.join(os.path.dirname(os.path.dirname(_clang() or "")), "lib", "clang", "*", "lib",
+                                  "linux", "libclang_rt.ubsan_standalone-x86_64.so"))
+    return libs[0] if libs else None
+
+
+def build_emulator(out_dir: str, source: str = KERNELS, ubsan: bool = False) -> str:
+    """Compile `source` with the wave emulator into out_dir/libw4a16_emu.so
+    (with `ubsan`, the kernel code under UndefinedBehaviorSanitizer, aborting
+    at the first finding: misaligned vector accesses, signed overflow, bad shifts)."""
     sys.path.insert(0, EMU)
     try:
         import prepare
@@ -75,8 +84,13 @@ def build_emulator(out_dir: str, source: str = KERNELS) -> str:
     inc = [f"-I{EMU}", f"-I{os.path.join(ROOT, 'inf-engine_amd', 'csrc')}", f"-I{os.path.join(ROOT, 'include')}"]
     # The emulator (MFMA arithmetic, fiber switches) optimized; the kernel TU at
     # -O0: it builds in seconds instead of a minute and runs about 1.5x slower.
+    san = []
+    if ubsan:
+        rt_lib = _ubsan_runtime()
+        san = ["-fsanitize=undefined", "-fno-sanitize-recover=undefined", "-shared-libsan",
+               f"-Wl,-rpath,{os.path.dirname(rt_lib)}"]
     for cmd in ([_clang(), "-O2", "-std=c++17", "-fPIC", "-c", *inc, os.path.join(EMU, "emu_runtime.cpp"), "-o", rt],
-                [_clang(), "-O0", "-g", "-std=c++17", "-shared", "-fPIC", *inc, tu, rt, "-o", lib]):
+                [_clang(), "-O0", "-g", "-std=c++17", "-shared", "-fPIC", *san, *inc, tu, rt, "-o", lib]):
         res = subprocess.run(cmd, capture_output=True, text=True)
         assert res.returncode == 0, res.stdout + res.stderr
     return lib
@@ -570,3 +584,36 @@ def test_split_k_give_up_path(emu):
     assert lib.w4a16_linear(xp, k, pp, n, sp, n, y2, n, m, n, k, 128, ws, size, None) == 0
     assert np.array_equal(emu.get(y2, (m, n), np.uint16), ref)
     assert emu.slots_clear(ws, size)
+
+
+def test_kernels_under_undefined_behavior_sanitizer(tmp_path):
+    """The kernel code built with UndefinedBehaviorSanitizer (alignment of every
+    vector access, signed overflow, shifts) on planner-branch shapes, the
+    misaligned-operand cases and every other entry point, in a child process
+    so that a finding (which aborts) fails this test with its report."""
+    if _clang() is None or _ubsan_runtime() is None:
+        pytest.skip("clang++ with the UBSan runtime not available")
+    lib = build_emulator(str(tmp_path), ubsan=True)
+    script = textwrap.dedent(f"""
+        import sys
+        sys.path[:0] = [{ROOT!r}, {os.path.join(ROOT, 'tests')!r}]
+        import test_emulated_kernels as T
+        emu = T.Emu({lib!r})
+        for m, k, n in T.SHAPES[::2]:
+            T.test_linear_matches_oracle(emu, m, k, n)
+        for m in (5, 40):
+            T.test_linear_strided_unaligned_and_sliced(emu, m)
+        for case in range(24):
+            T.test_guarded_misaligned_operands(emu, case)
+        T.test_grouped_matches_oracle(emu)
+        for a in [(5, 512, 384), (256, 512, 1024), (130, 512, 200)]:
+            T.test_swiglu_matches_oracle(emu, *a)
+        for a in [(1, 1000, 4096), (9, 200, 512)]:
+            T.test_bf16_gemv_matches_oracle(emu, *a)
+        T.test_dequant_bit_exact(emu)
+        T.test_noalloc_matches_linear(emu)
+        print("ubsan clean")
+    """)
+    res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=900)
+    assert res.returncode == 0 and "ubsan clean" in res.stdout, res.stdout[-2000:] + res.stderr[-4000:]
+

@@ -24,6 +24,20 @@ def test_slot_protocol_host_emulation(tmp_path):
     assert res.returncode == 0 and res.stdout.strip().endswith("ok"), res.stdout + res.stderr
 
 
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_slot_protocol_host_emulation_under_thread_sanitizer(tmp_path):
+    """The threaded emulation built with ThreadSanitizer: publishers, finisher and
+    late publishers touch the slots only through atomics."""
+    exe = tmp_path / "slot_emu_tsan"
+    src = os.path.join(ROOT, "tests", "native", "slot_protocol_emu.cpp")
+    inc = os.path.join(ROOT, "inf-engine_amd", "csrc")
+    subprocess.run(["g++", "-O1", "-g", "-std=c++17", "-pthread", "-fsanitize=thread", "-I", inc, src, "-o", str(exe)],
+                   check=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0 and res.stdout.strip().endswith("ok"), res.stdout + res.stderr
+    assert "WARNING: ThreadSanitizer" not in res.stderr, res.stderr
+
+
 def test_status_offset_and_spin_limit_api(native_lib):
     from w4a16 import _native as nat
     import ctypes
