@@ -77,7 +77,9 @@ const char* w4a16_error_string(int code);
 
 /*
  * Bytes of device workspace w4a16_linear needs for an (M, N, K) call; 0 means
- * the call needs none.  A workspace of W bytes is used in two halves: the
+ * the call needs none.  The size covers any operand alignment (activations
+ * whose rows are not 16-byte aligned run M > 32 through the decode kernel 32
+ * rows at a time, which can need more than the GEMM).  A workspace of W bytes is used in two halves: the
  * lower half holds the decode kernels' split-K partial slots, which must be
  * zero before the first call that uses the buffer and are left at zero by
  * every completed call; the upper half is GEMM scratch.  So: zero a buffer

@@ -1912,11 +1912,20 @@ int w4a16_workspace_size(int M, int N, int K, int group_size, size_t* bytes) {
   if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
   if (group_size != kGroup) return W4A16_ERR_GROUP_SIZE;
   if (K % kGroup != 0) return W4A16_ERR_K_GROUP;
-  // Sized for contiguous, 256-byte aligned operands (what the wrapper passes).
+  // The query sees shapes, not pointers.  Activations whose rows are not
+  // 16-byte aligned send M > 32 through the decode kernel 32 rows at a time
+  // (separate()), which can need more split-K slots than the GEMM plan of
+  // aligned rows, so the size covers both.
   const uintptr_t a = 256;
-  const w4a16_problem q{reinterpret_cast<const void*>(a), K, reinterpret_cast<const int8_t*>(a), N,
-                        reinterpret_cast<const float*>(a), N, reinterpret_cast<void*>(a), N, M, N, K};
-  return workspace_for(&q, 1, bytes);
+  w4a16_problem q{reinterpret_cast<const void*>(a), K, reinterpret_cast<const int8_t*>(a), N,
+                  reinterpret_cast<const float*>(a), N, reinterpret_cast<void*>(a), N, M, N, K};
+  int rc = workspace_for(&q, 1, bytes);
+  if (rc != W4A16_OK) return rc;
+  q.x = reinterpret_cast<const void*>(a + 2);
+  size_t unaligned = 0;
+  rc = workspace_for(&q, 1, &unaligned);
+  *bytes = std::max(*bytes, unaligned);
+  return rc;
 }
 
 int w4a16_status_offset(size_t workspace_bytes, size_t* offset) {
@@ -1975,11 +1984,18 @@ int w4a16_workspace_size_swiglu(int M, int N, int K, int group_size, size_t* byt
   if (M < 0 || N < 0 || K < 0) return W4A16_ERR_SHAPE;
   if (group_size != kGroup) return W4A16_ERR_GROUP_SIZE;
   if (K % kGroup != 0) return W4A16_ERR_K_GROUP;
+  // Aligned and unaligned activation rows, as in w4a16_workspace_size.
   const uintptr_t a = 256;
-  const w4a16_problem q{reinterpret_cast<const void*>(a), K, reinterpret_cast<const int8_t*>(a), N,
-                        reinterpret_cast<const float*>(a), N, reinterpret_cast<void*>(a), N, M, N, K};
-  const w4a16_problem pair[2] = {q, q};
-  return swiglu_workspace(pair, bytes);
+  w4a16_problem q{reinterpret_cast<const void*>(a), K, reinterpret_cast<const int8_t*>(a), N,
+                  reinterpret_cast<const float*>(a), N, reinterpret_cast<void*>(a), N, M, N, K};
+  w4a16_problem pair[2] = {q, q};
+  int rc = swiglu_workspace(pair, bytes);
+  if (rc != W4A16_OK) return rc;
+  pair[0].x = pair[1].x = reinterpret_cast<const void*>(a + 2);
+  size_t unaligned = 0;
+  rc = swiglu_workspace(pair, &unaligned);
+  *bytes = std::max(*bytes, unaligned);
+  return rc;
 }
 
 int w4a16_swiglu(const void* x, int64_t ldx, const int8_t* gate_packed, int64_t gate_ldp, const float* gate_scale,

@@ -119,15 +119,23 @@ class Emu:
         lib.w4a16_linear_grouped.argtypes = [ctypes.POINTER(_native.Problem), i32, i32, vp, sz, vp]
         lib.w4a16_workspace_size_grouped.argtypes = [ctypes.POINTER(_native.Problem), i32, i32, ctypes.POINTER(sz)]
 
-    def put(self, arr: np.ndarray, extra: int = 0) -> int:
-        """Copy arr into a buffer that ends `extra` bytes after the array."""
+    def _aligned(self, nbytes: int) -> int:
+        """A 16-byte aligned buffer of nbytes whose end is within 15 bytes of the
+        trailing guard page (buffers end at a page boundary, so the start is
+        -size mod 16 without the pad)."""
+        p = self.lib.emu_alloc(nbytes + (-nbytes) % 16)
+        assert p % 16 == 0
+        return p
+
+    def put(self, arr: np.ndarray) -> int:
+        """Copy arr into a 16-byte aligned guarded buffer (as a device allocation is)."""
         a = np.ascontiguousarray(arr)
-        p = self.lib.emu_alloc(a.nbytes + extra)
+        p = self._aligned(a.nbytes)
         ctypes.memmove(p, a.ctypes.data, a.nbytes)
         return p
 
     def zeros(self, nbytes: int) -> int:
-        p = self.lib.emu_alloc(nbytes)
+        p = self._aligned(nbytes)
         ctypes.memset(p, 0, nbytes)
         return p
 
@@ -196,9 +204,9 @@ def run_linear(emu, xb, packed, scale, m, k, n, misalign_x=False, check_ws=True)
     nb = ws_bytes.value + (4096 if ws_bytes.value else 0)
     ws, nb = emu.workspace(nb)
     if misalign_x:
-        # One element off 16-byte alignment: the generic-load path.
-        base = emu.put(np.concatenate([np.zeros(1, np.uint16), xb.reshape(-1)]))
-        xp = base + 2
+        # One element off 16-byte alignment: the generic-load path (and, for M > 32,
+        # the decode kernel in 32-row chunks).
+        xp = _place(emu, xb, 2, front=False)
     else:
         xp = emu.put(xb)
     y = emu.zeros(m * n * 2)
@@ -453,15 +461,23 @@ def test_schedule_check_finds_a_missing_barrier(tmp_path):
 
 
 def _place(emu, arr, misalign: int, front: bool) -> int:
-    """Copy arr to a guarded buffer, `misalign` bytes after its start; the guard
-    page follows the data (front=False) or precedes the buffer (front=True)."""
+    """Copy arr to a guarded buffer so that its first byte sits `misalign` bytes
+    past a 16-byte boundary.  front=False: the data ends within 16 bytes of the
+    trailing guard page (exactly at it when the sizes allow); front=True: the
+    buffer starts right after the leading guard page."""
     a = np.ascontiguousarray(arr)
-    alloc = emu.lib.emu_alloc_front if front else emu.lib.emu_alloc
-    alloc.restype = ctypes.c_void_p
-    alloc.argtypes = [ctypes.c_size_t]
-    p = alloc(a.nbytes + misalign)
-    ctypes.memmove(p + misalign, a.ctypes.data, a.nbytes)
-    return p + misalign
+    if front:
+        emu.lib.emu_alloc_front.restype = ctypes.c_void_p
+        emu.lib.emu_alloc_front.argtypes = [ctypes.c_size_t]
+        p = emu.lib.emu_alloc_front(a.nbytes + misalign) + misalign
+    else:
+        # The buffer ends at a page boundary, so its start is -size (mod 16):
+        # pad the size until the start lands `misalign` past a 16-byte boundary.
+        pad = (-a.nbytes - misalign) % 16
+        p = emu.lib.emu_alloc(a.nbytes + pad)
+    assert p % 16 == misalign % 16
+    ctypes.memmove(p, a.ctypes.data, a.nbytes)
+    return p
 
 
 def _rows_with_stride(rows, cols, ld, dtype, fill):

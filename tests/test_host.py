@@ -138,8 +138,10 @@ def test_workspace_planning(native_lib):
 
     # M=1 Qwen3-8B gate: 8 K splits, 7 published fp32 partial slots [7, 1, N] in the lower half.
     assert half(ws(1, 12288, 4096)) == 7 * 12288 * 4
-    # Large M: per-(group, row) correction sums in the upper half.
-    assert half(ws(2048, 12288, 4096)) == 32 * 2048 * 4
+    # Large M: the GEMM needs only the per-(group, row) correction sums (32 * 2048 * 4 B in the
+    # upper half), but activations off 16-byte alignment run 32-row decode chunks whose 3
+    # published slots of [32, N] are larger, and the size query covers both.
+    assert half(ws(2048, 12288, 4096)) == max(32 * 2048 * 4, 3 * 32 * 12288 * 4)
     with pytest.raises(AssertionError):
         ws(1, 4096, 4096, 64)
     with pytest.raises(ValueError):
@@ -152,6 +154,33 @@ def test_workspace_planning(native_lib):
                 if b:
                     slots = half(b) // (m * n * 4)  # nsplit - 1, rounded down by the 256-B alignment
                     assert 1 <= slots + (1 if half(b) % (m * n * 4) else 0) <= (k // 128 + 3) // 4
+
+
+def test_workspace_query_covers_unaligned_activations(native_lib):
+    """w4a16_workspace_size sees only shapes; it must cover the plan of a call whose
+    activation rows are off 16-byte alignment (M > 32 then runs the decode kernel 32
+    rows at a time) as well as the aligned plan.  The grouped query, which sees the
+    pointers, gives each plan's exact size."""
+    from w4a16 import _native as nat
+
+    lib = native_lib
+    exact = ctypes.c_size_t(0)
+
+    def grouped(m, n, k, x):
+        q = (nat.Problem * 1)()
+        q[0] = nat.Problem(x, k, 4096, n, 4096, n, 4096, n, m, n, k)
+        assert lib.w4a16_workspace_size_grouped(q, 1, 128, ctypes.byref(exact)) == nat.W4A16_OK
+        return exact.value
+
+    short = 0
+    for m in (1, 16, 32, 33, 40, 64, 65, 129, 300, 2048, 4096):
+        for k in (128, 1024, 4096, 5120, 12288, 25600):
+            for n in (64, 1000, 1024, 4096, 12288, 25600):
+                size = nat.workspace_size(m, n, k)
+                aligned, unaligned = grouped(m, n, k, 4096), grouped(m, n, k, 4098)
+                assert size >= aligned and size >= unaligned, (m, n, k, size, aligned, unaligned)
+                short += unaligned > aligned
+    assert short > 0  # the unaligned plan is the larger one for some shapes (e.g. M=33, K=4096, N=25600)
 
 
 def test_swiglu_workspace_and_validation(native_lib):
