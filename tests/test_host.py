@@ -102,9 +102,11 @@ def test_grouped_argument_validation(native_lib):
     # Mixed M: the decode and GEMM batches share one workspace, sized for the larger.
     mixed = (nat.Problem * 2)(table[0], nat.Problem(16, 4096, 16, 4096, 16, 4096, 16, 4096, 2048, 4096, 4096))
     assert lib.w4a16_workspace_size_grouped(mixed, 2, 128, ctypes.byref(size)) == nat.W4A16_OK
-    decode_only = ctypes.c_size_t(0)
+    decode_only, gemm_only = ctypes.c_size_t(0), ctypes.c_size_t(0)
     assert lib.w4a16_workspace_size_grouped(table, 1, 128, ctypes.byref(decode_only)) == nat.W4A16_OK
-    assert size.value == max(decode_only.value, nat.workspace_size(2048, 4096, 4096))
+    gemm = (nat.Problem * 1)(mixed[1])
+    assert lib.w4a16_workspace_size_grouped(gemm, 1, 128, ctypes.byref(gemm_only)) == nat.W4A16_OK
+    assert size.value == max(decode_only.value, gemm_only.value)
 
 
 def test_dequant_argument_validation(native_lib):
