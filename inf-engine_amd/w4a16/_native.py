@@ -159,6 +159,20 @@ def _rows(t: torch.Tensor) -> tuple[torch.Tensor, int]:
     return t, (t.stride(0) if rows > 1 else max(t.stride(0), width))
 
 
+def _activations(a: torch.Tensor, always: bool = False) -> tuple[torch.Tensor, int]:
+    """``_rows`` for activations, copied to a fresh (aligned) tensor when their
+    rows are not 16-byte aligned (data pointer or row stride) and M > 32, or
+    whenever ``always``.  The GEMM stages x with 16-byte copies; given such rows
+    the C entry points run M > 32 through the decode kernel 32 rows at a time,
+    and every chunk streams all of the weights again, so one copy of x is far
+    cheaper.  The lm_head GEMV takes aligned rows only (``always``)."""
+    a, ld = _rows(a)
+    if (always or a.shape[0] > 32) and (a.data_ptr() % 16 or ld % 8):
+        a = a.clone(memory_format=torch.contiguous_format)
+        ld = a.shape[1]
+    return a, ld
+
+
 def workspace_size(m: int, n: int, k: int, group_size: int = 128) -> int:
     out = ctypes.c_size_t(0)
     check(load_library().w4a16_workspace_size(m, n, k, group_size, ctypes.byref(out)), "w4a16_workspace_size")
@@ -278,7 +292,7 @@ def linear(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_siz
     lib = load_library()
     m, k = a.shape
     n = packed.shape[1]
-    a, ldx = _rows(a)
+    a, ldx = _activations(a)
     packed, ldp = _rows(packed)
     scale, lds = _rows(scale)
     y = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
@@ -321,8 +335,11 @@ def linear_grouped(xs, weights, group_size: int) -> list[torch.Tensor]:
         raise ValueError(f"a grouped call takes 1..{MAX_PROBLEMS} projections, got {len(weights)}")
     table = (Problem * len(weights))()
     outs, keep = [], []
+    rows = {}  # one (possibly copied) view per distinct activation tensor, so shared x stays shared
     for i, (x, (packed, scale)) in enumerate(zip(xs, weights)):
-        x, ldx = _rows(x)
+        if id(x) not in rows:
+            rows[id(x)] = _activations(x)
+        x, ldx = rows[id(x)]
         packed, ldp = _rows(packed)
         scale, lds = _rows(scale)
         keep += [x, packed, scale]
@@ -348,7 +365,7 @@ def swiglu(a: torch.Tensor, gate, up, group_size: int) -> torch.Tensor:
     """h = silu(a @ Wg) * (a @ Wu) on the current HIP stream; gate/up are (packed, fp32 scale)."""
     lib = load_library()
     m, k = a.shape
-    a, ldx = _rows(a)
+    a, ldx = _activations(a)
     ops, lds_ = [], []
     for packed, scale in (gate, up):
         for t in (packed, scale):
@@ -379,7 +396,7 @@ def bf16_gemv(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     lib = load_library()
     m, k = x.shape
     n = w.shape[0]
-    x, ldx = _rows(x)
+    x, ldx = _activations(x, always=True)
     w, ldw = _rows(w)
     y = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
     stream = torch.cuda.current_stream(x.device).cuda_stream

@@ -512,3 +512,29 @@ def test_noalloc_entry_point_rejects_before_launch(native_lib):
     assert lib.w4a16_linear_noalloc(None, 4096, big, 4096, big, 4096, big, 4096, 1, 4096, 4096, 128,
                                     None) == nat.W4A16_ERR_NULL
     assert lib.w4a16_linear_noalloc(None, 0, None, 0, None, 0, None, 0, 0, 16, 128, 128, None) == nat.W4A16_OK
+
+
+def test_unaligned_activation_rows_are_copied_for_gemm_sized_m():
+    """The wrappers copy activation rows that are not 16-byte aligned (pointer or row
+    stride) once M > 32, instead of letting the C entry point stream the weights once per
+    32-row chunk; smaller M keeps the view (the decode kernel reads any alignment), and the
+    lm_head GEMV always gets aligned rows."""
+    from w4a16 import _native
+
+    base = torch.arange(70 * 256 + 8, dtype=torch.float32).to(torch.bfloat16)
+    for m in (33, 64, 2048 // 32):
+        view = base[1:1 + m * 256].view(m, 256)             # pointer 2 bytes off alignment
+        assert view.data_ptr() % 16 == 2
+        rows, ld = _native._activations(view)
+        assert rows.data_ptr() % 16 == 0 and ld == 256 and torch.equal(rows, view)
+    small = base[1:1 + 32 * 256].view(32, 256)
+    rows, ld = _native._activations(small)
+    assert rows.data_ptr() == small.data_ptr() and ld == 256
+    strided = base[: 40 * 257].view(40, 257)[:, :256]         # row stride 257: not a multiple of 8
+    rows, ld = _native._activations(strided)
+    assert ld == 256 and rows.data_ptr() % 16 == 0 and torch.equal(rows, strided)
+    one = base[1:257].view(1, 256)
+    rows, ld = _native._activations(one, always=True)
+    assert rows.data_ptr() % 16 == 0 and torch.equal(rows, one)
+    aligned = base[:64 * 256].view(64, 256)
+    assert _native._activations(aligned)[0].data_ptr() == aligned.data_ptr()
