@@ -633,3 +633,93 @@ def test_kernels_under_undefined_behavior_sanitizer(tmp_path):
     res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=900)
     assert res.returncode == 0 and "ubsan clean" in res.stdout, res.stdout[-2000:] + res.stderr[-4000:]
 
+
+
+@pytest.fixture
+def wrappers_on_emulator(emu, monkeypatch):
+    """w4a16._native bound to the emulated library, driven with CPU tensors: the
+    wrappers' view handling (row strides, overlapping rows, column slices,
+    unaligned rows, grouped tables, SwiGLU operand order) runs unchanged and the
+    kernels read host memory."""
+    from types import SimpleNamespace
+
+    import torch
+
+    from w4a16 import _native
+
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "LIB_PATH", emu.lib._name)
+    monkeypatch.setattr(_native, "_workspaces", {})
+    monkeypatch.setattr(_native, "_retired", [])
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda device=None: SimpleNamespace(cuda_stream=0))
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: 0)
+    yield _native
+    _native._lib = None  # the next load_library() loads the real library again
+
+
+def _torch_problem(m, k, n, seed):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    packed = torch.randint(-128, 128, (k // 2, n), generator=g, dtype=torch.int8)
+    scale = torch.rand(k // 128, n, generator=g) * 0.01 + 0.001
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    return x, packed, scale
+
+
+def _ref(x, packed, scale):
+    return orc.fused_reference(x.float().numpy(), packed.numpy(), scale.numpy())
+
+
+def test_wrappers_handle_views(wrappers_on_emulator):
+    import torch
+
+    nat = wrappers_on_emulator
+    k, n = 1024, 384
+    for m in (1, 5, 40, 130):
+        x, packed, scale = _torch_problem(m, k, n, seed=m)
+        ref = _ref(x, packed, scale)
+        views = {
+            "contiguous": x,
+            "row stride K+8": torch.nn.functional.pad(x, (0, 8))[:, :k],
+            "row stride K+3": torch.nn.functional.pad(x, (0, 3))[:, :k],
+            "pointer off alignment": torch.cat([torch.zeros(1, dtype=x.dtype), x.reshape(-1)])[1:].view(m, k),
+            "transposed": x.t().contiguous().t(),
+        }
+        for name, v in views.items():
+            y = nat.linear(v, packed, scale, 128)
+            assert_parity(y.float().numpy().astype(np.float64), ref, f"linear M={m} {name}")
+        wide_p = torch.nn.functional.pad(packed, (0, 16))
+        wide_s = torch.nn.functional.pad(scale, (0, 4))
+        y = nat.linear(x, wide_p[:, :n], wide_s[:, :n], 128)
+        assert_parity(y.float().numpy().astype(np.float64), ref, f"linear M={m} column-sliced weights")
+    x1, packed, scale = _torch_problem(1, k, n, seed=99)
+    y = nat.linear(x1[0].expand(6, k), packed, scale, 128)  # overlapping rows (row stride 0)
+    assert_parity(y.float().numpy().astype(np.float64), np.repeat(_ref(x1, packed, scale), 6, axis=0), "expand")
+
+
+def test_wrappers_grouped_swiglu_and_gemv(wrappers_on_emulator):
+    import torch
+
+    nat = wrappers_on_emulator
+    k = 512
+    x, p0, s0 = _torch_problem(36, k, 256, seed=1)
+    _, p1, s1 = _torch_problem(36, k, 128, seed=2)
+    xo = torch.cat([torch.zeros(1, dtype=x.dtype), x.reshape(-1)])[1:].view(36, k)  # shared, unaligned
+    outs = nat.linear_grouped([xo, xo], [(p0, s0), (p1, s1)], 128)
+    for y, (p, s) in zip(outs, [(p0, s0), (p1, s1)]):
+        assert_parity(y.float().numpy().astype(np.float64), _ref(x, p, s), "grouped shared unaligned x")
+    for m in (3, 130):
+        xs, gp, gs = _torch_problem(m, k, 256, seed=10 + m)
+        _, up, us = _torch_problem(m, k, 256, seed=20 + m)
+        h = nat.swiglu(xs, (gp, gs), (up, us), 128)
+        ref = orc.swiglu_reference(xs.float().numpy(), (gp.numpy(), gs.numpy()), (up.numpy(), us.numpy()))
+        assert_parity(h.float().numpy().astype(np.float64), ref, f"swiglu M={m}", roundings=1 if m <= 64 else 6)
+    g = torch.Generator().manual_seed(5)
+    xg = torch.randn(3, 1024, generator=g).to(torch.bfloat16)
+    w = (torch.randn(200, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    xg_off = torch.cat([torch.zeros(1, dtype=xg.dtype), xg.reshape(-1)])[1:].view(3, 1024)
+    y = nat.bf16_gemv(xg_off, w)  # unaligned rows are copied for the GEMV
+    ref = xg.double().numpy() @ w.double().numpy().T
+    assert_parity(y.float().numpy().astype(np.float64), ref, "bf16_gemv unaligned x")
