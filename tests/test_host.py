@@ -461,23 +461,60 @@ def _gemm_copy_wait_paths(asm: str, func: str) -> list[str]:
     return bad
 
 
-def test_gemm_streamed_loads_cover_the_copy_wait(tmp_path):
-    """Every full-tile GEMM instantiation issues >= 17 loads between its activation copies and
-    the vmcnt(17) wait that publishes them (the source's kLoadsAfterA), on every path."""
+@pytest.fixture(scope="module")
+def gfx950_asm(tmp_path_factory):
+    """The library's gfx950 assembly, compiled with the build's own flags."""
     import shutil
     import subprocess
-    import sys
 
     from w4a16 import build as B
 
     if not os.path.exists(B.HIPCC) and shutil.which("hipcc") is None:
         pytest.skip("hipcc not available")
-    out = tmp_path / "k.s"
+    out = tmp_path_factory.mktemp("asm") / "k.s"
     flags = [f for f in B.FLAGS if f not in ("-fPIC", "-shared")]
     res = subprocess.run([B.HIPCC, *flags, "--cuda-device-only", "-S", *B.SOURCES, "-o", str(out)],
                          capture_output=True, text=True)
     assert res.returncode == 0, res.stderr[-2000:]
-    asm = out.read_text()
+    return out.read_text()
+
+
+def _kernel_resources(asm: str) -> dict[str, dict[str, int]]:
+    """name -> {vgpr, spill bytes (private segment), lds} from the code object metadata."""
+    out = {}
+    for m in re.finditer(r"\.name:\s+(\S+)\n((?:.*\n){0,40})", asm):
+        blk = m.group(2)
+        v = re.search(r"\.vgpr_count:\s+(\d+)", blk)
+        p = re.search(r"\.private_segment_fixed_size:\s+(\d+)", blk)
+        if v and p:
+            out[m.group(1)] = {"vgpr": int(v.group(1)), "spill": int(p.group(1))}
+    return out
+
+
+def test_hot_kernels_keep_their_register_budget(gfx950_asm):
+    """The measured speed of the hot kernels rests on their occupancy: the full-tile GEMMs
+    hold two waves per SIMD (at most 256 VGPRs, no spills), the batch-1 decode kernels five
+    (at most 96 VGPRs), and no full-tile decode kernel spills.  A compiler change or an edit
+    that breaks this shows up here rather than as an unexplained slowdown."""
+    res = _kernel_resources(gfx950_asm)
+    gemm = {k: v for k, v in res.items() if re.search(r"gemm_kernelILi\dELb1E", k)}
+    decode_full = {k: v for k, v in res.items() if re.search(r"gemv_kernelILi\dELi\dELb1E", k)}
+    decode_m1 = {k: v for k, v in decode_full.items() if "ELi1ELb" in k}
+    assert len(gemm) >= 4 and len(decode_full) >= 20 and len(decode_m1) >= 4, (len(gemm), len(decode_full))
+    for name, r in gemm.items():
+        assert r["vgpr"] <= 256 and r["spill"] == 0, (name, r)
+    for name, r in decode_full.items():
+        assert r["spill"] == 0, (name, r)
+    for name, r in decode_m1.items():
+        assert r["vgpr"] <= 96, (name, r)
+
+
+def test_gemm_streamed_loads_cover_the_copy_wait(gfx950_asm):
+    """Every full-tile GEMM instantiation issues >= 17 loads between its activation copies and
+    the vmcnt(17) wait that publishes them (the source's kLoadsAfterA), on every path."""
+    import sys
+
+    asm = gfx950_asm
     funcs = sorted(set(re.findall(r"^(_Z\w*gemm_kernelILi\dELb1E\w*):", asm, re.M)))
     assert len(funcs) >= 4, funcs  # CPL 2 / 4, two K halves, the SwiGLU pair
     for f in funcs:
