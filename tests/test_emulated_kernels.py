@@ -35,7 +35,6 @@ from __future__ import annotations
 
 import ctypes
 import os
-import shutil
 import subprocess
 import sys
 import textwrap
@@ -46,130 +45,13 @@ import pytest
 from oracle import int4_oracle as orc
 from oracle.tolerance import assert_parity
 
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-EMU = os.path.join(ROOT, "tests", "native", "emu")
-KERNELS = os.path.join(ROOT, "inf-engine_amd", "csrc", "w4a16_kernels.hip")
-
-
-def _clang() -> str | None:
-    for c in ("/opt/rocm/llvm/bin/clang++", shutil.which("clang++")):
-        if c and os.path.exists(c):
-            return c
-    return None
-
-
-def _ubsan_runtime() -> str | None:
-    import glob
-    libs = glob.glob(os.path.join(os.path.dirname(os.path.dirname(_clang() or "")), "lib", "clang", "*", "lib",
-                                  "linux", "libclang_rt.ubsan_standalone-x86_64.so"))
-    return libs[0] if libs else None
-
-
-def build_emulator(out_dir: str, source: str = KERNELS, ubsan: bool = False) -> str:
-    """Compile `source` with the wave emulator into out_dir/libw4a16_emu.so
-    (with `ubsan`, the kernel code under UndefinedBehaviorSanitizer, aborting
-    at the first finding: misaligned vector accesses, signed overflow, bad shifts)."""
-    sys.path.insert(0, EMU)
-    try:
-        import prepare
-    finally:
-        sys.path.remove(EMU)
-    tu = os.path.join(out_dir, "w4a16_host.cpp")
-    with open(source) as f:
-        text = prepare.transform(f.read())
-    with open(tu, "w") as f:
-        f.write(text)
-    lib = os.path.join(out_dir, "libw4a16_emu.so")
-    rt = os.path.join(out_dir, "emu_runtime.o")
-    inc = [f"-I{EMU}", f"-I{os.path.join(ROOT, 'inf-engine_amd', 'csrc')}", f"-I{os.path.join(ROOT, 'include')}"]
-    # The emulator (MFMA arithmetic, fiber switches) optimized; the kernel TU at
-    # -O0: it builds in seconds instead of a minute and runs about 1.5x slower.
-    san = []
-    if ubsan:
-        rt_lib = _ubsan_runtime()
-        san = ["-fsanitize=undefined", "-fno-sanitize-recover=undefined", "-shared-libsan",
-               f"-Wl,-rpath,{os.path.dirname(rt_lib)}"]
-    for cmd in ([_clang(), "-O2", "-std=c++17", "-fPIC", "-c", *inc, os.path.join(EMU, "emu_runtime.cpp"), "-o", rt],
-                [_clang(), "-O0", "-g", "-std=c++17", "-shared", "-fPIC", *san, *inc, tu, rt, "-o", lib]):
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        assert res.returncode == 0, res.stdout + res.stderr
-    return lib
-
-
-class Emu:
-    """ctypes view of the emulated library plus guarded host 'device' buffers."""
-
-    def __init__(self, path: str):
-        self.lib = lib = ctypes.CDLL(path)
-        vp, i64, i32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
-        lib.emu_alloc.restype = vp
-        lib.emu_alloc.argtypes = [sz]
-        lib.w4a16_linear.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp, sz, vp]
-        lib.w4a16_linear_noalloc.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
-        lib.w4a16_workspace_size.argtypes = [i32, i32, i32, i32, ctypes.POINTER(sz)]
-        lib.w4a16_swiglu.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64,
-                                     i32, i32, i32, i32, vp, sz, vp]
-        lib.w4a16_workspace_size_swiglu.argtypes = [i32, i32, i32, i32, ctypes.POINTER(sz)]
-        lib.w4a16_bf16_gemv.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, vp]
-        lib.w4a16_dequant.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
-        lib.w4a16_status_offset.argtypes = [sz, ctypes.POINTER(sz)]
-        sys.path.insert(0, os.path.join(ROOT, "inf-engine_amd"))
-        from w4a16 import _native
-        self.Problem = _native.Problem
-        lib.w4a16_linear_grouped.argtypes = [ctypes.POINTER(_native.Problem), i32, i32, vp, sz, vp]
-        lib.w4a16_workspace_size_grouped.argtypes = [ctypes.POINTER(_native.Problem), i32, i32, ctypes.POINTER(sz)]
-
-    def _aligned(self, nbytes: int) -> int:
-        """A 16-byte aligned buffer of nbytes whose end is within 15 bytes of the
-        trailing guard page (buffers end at a page boundary, so the start is
-        -size mod 16 without the pad)."""
-        p = self.lib.emu_alloc(nbytes + (-nbytes) % 16)
-        assert p % 16 == 0
-        return p
-
-    def put(self, arr: np.ndarray) -> int:
-        """Copy arr into a 16-byte aligned guarded buffer (as a device allocation is)."""
-        a = np.ascontiguousarray(arr)
-        p = self._aligned(a.nbytes)
-        ctypes.memmove(p, a.ctypes.data, a.nbytes)
-        return p
-
-    def zeros(self, nbytes: int) -> int:
-        p = self._aligned(nbytes)
-        ctypes.memset(p, 0, nbytes)
-        return p
-
-    def get(self, p: int, shape, dtype) -> np.ndarray:
-        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
-        return np.frombuffer(ctypes.string_at(p, n), dtype=dtype).reshape(shape).copy()
-
-    def workspace(self, nbytes: int) -> tuple[int | None, int]:
-        return (self.zeros(nbytes), nbytes) if nbytes else (None, 0)
-
-    def slots_clear(self, ws: int | None, nbytes: int) -> bool:
-        """Lower (slot) half zero and status word clear."""
-        if not ws:
-            return True
-        half = (nbytes // 2) & ~255
-        off = ctypes.c_size_t(0)
-        assert self.lib.w4a16_status_offset(nbytes, ctypes.byref(off)) == 0
-        low = self.get(ws, (half,), np.uint8)
-        status = self.get(ws + off.value, (1,), np.uint32)[0]
-        return not low.any() and status == 0
-
-
-def bf16_bits(x: np.ndarray) -> np.ndarray:
-    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
-    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-
-
-def bf16_value(b: np.ndarray) -> np.ndarray:
-    return (b.astype(np.uint32) << 16).view(np.float32)
+from emu_harness import (KERNELS, ROOT, Emu, bf16_bits, bf16_value, build_emulator, clang, place, problem, reference,
+                         rows_with_stride, run_linear, set_concurrency, set_schedule, ubsan_runtime)
 
 
 @pytest.fixture(scope="module")
 def emu(tmp_path_factory):
-    if _clang() is None:
+    if clang() is None:
         pytest.skip("clang++ not available")
     return Emu(build_emulator(str(tmp_path_factory.mktemp("emu"))))
 
@@ -180,45 +62,6 @@ def _release_buffers(request):
     yield
     if "emu" in request.fixturenames:
         request.getfixturevalue("emu").lib.emu_free_all()
-
-
-def problem(m, k, n, seed, pad_x=0, pad_w=0, quantized=False):
-    """x (bf16 bits, [m, k + pad_x]), packed [k/2, n + pad_w], scale [k/128, n + pad_w]."""
-    rng = np.random.default_rng(seed)
-    if quantized:
-        w = (rng.standard_normal((k, n + pad_w)) * 0.02).astype(np.float32)
-        packed, scale = orc.quantize(w)
-    else:
-        packed = rng.integers(-128, 128, size=(k // 2, n + pad_w), dtype=np.int8)
-        scale = (rng.random((k // 128, n + pad_w), dtype=np.float32) * 0.01 + 0.001).astype(np.float32)
-    xb = bf16_bits(rng.standard_normal((m, k + pad_x)).astype(np.float32))
-    return xb, packed, scale
-
-
-def run_linear(emu, xb, packed, scale, m, k, n, misalign_x=False, check_ws=True):
-    lib = emu.lib
-    ldx, ldp, lds = xb.shape[1], packed.shape[1], scale.shape[1]
-    ws_bytes = ctypes.c_size_t(0)
-    assert lib.w4a16_workspace_size(m, n, k, 128, ctypes.byref(ws_bytes)) == 0
-    # Round the workspace to what _native would pass (it only grows), with slack.
-    nb = ws_bytes.value + (4096 if ws_bytes.value else 0)
-    ws, nb = emu.workspace(nb)
-    if misalign_x:
-        # One element off 16-byte alignment: the generic-load path (and, for M > 32,
-        # the decode kernel in 32-row chunks).
-        xp = _place(emu, xb, 2, front=False)
-    else:
-        xp = emu.put(xb)
-    y = emu.zeros(m * n * 2)
-    rc = lib.w4a16_linear(xp, ldx, emu.put(packed), ldp, emu.put(scale), lds, y, n, m, n, k, 128, ws, nb, None)
-    assert rc == 0, rc
-    if check_ws:
-        assert emu.slots_clear(ws, nb), "workspace slot half or status word not clear after the call"
-    return emu.get(y, (m, n), np.uint16)
-
-
-def reference(xb, packed, scale, m, k, n):
-    return orc.fused_reference(bf16_value(xb[:, :k]), packed[:, :n], scale[:, :n])
 
 
 # Shapes across the planner's branches: batch-1 decode, split / unsplit K,
@@ -377,7 +220,7 @@ def test_guard_pages_catch_an_out_of_bounds_kernel(tmp_path, emu):
     script = textwrap.dedent(f"""
         import ctypes, sys
         sys.path[:0] = [{ROOT!r}, {os.path.join(ROOT, 'tests')!r}]
-        from test_emulated_kernels import Emu, problem
+        from emu_harness import Emu, problem
         emu = Emu({lib_path!r})
         m, k, n = 3, 512, 256
         xb, packed, scale = problem(m, k, n, seed=1)
@@ -397,7 +240,7 @@ def test_late_lds_copies_are_modelled(tmp_path):
     """Negative control for the direct-to-LDS model: a GEMM whose copy wait leaves one
     operation too many outstanding (vmcnt(18) instead of 17) reads activation tiles
     before they land, and the emulated result is wrong."""
-    if _clang() is None:
+    if clang() is None:
         pytest.skip("clang++ not available")
     with open(KERNELS) as f:
         src = f.read()
@@ -410,11 +253,6 @@ def test_late_lds_copies_are_modelled(tmp_path):
     y = run_linear(emu, xb, packed, scale, m, k, n)
     with pytest.raises(AssertionError):
         assert_parity(bf16_value(y).astype(np.float64), reference(xb, packed, scale, m, k, n), "short wait")
-
-
-def _set_schedule(emu, mode, seed=0):
-    emu.lib.emu_set_schedule.argtypes = [ctypes.c_int, ctypes.c_uint64]
-    emu.lib.emu_set_schedule(mode, seed)
 
 
 SCHEDULE_SHAPES = [(1, 1024, 512), (3, 4096, 1024), (16, 2048, 512), (24, 1024, 640), (40, 512, 320),
@@ -431,18 +269,18 @@ def test_results_do_not_depend_on_thread_schedule(emu):
             xb, packed, scale = problem(m, k, n, seed=m)
             outs = []
             for i, mode in enumerate((0, 1, 2, 2)):
-                _set_schedule(emu, mode, 7 + i)
+                set_schedule(emu, mode, 7 + i)
                 outs.append(run_linear(emu, xb, packed, scale, m, k, n))
             for o in outs[1:]:
                 assert np.array_equal(outs[0], o), f"schedule-dependent result at M={m} K={k} N={n}"
     finally:
-        _set_schedule(emu, 0)
+        set_schedule(emu, 0)
 
 
 def test_schedule_check_finds_a_missing_barrier(tmp_path):
     """Negative control: without the barrier between the decode kernel's LDS
     stores of wave totals and their sum, the result depends on the schedule."""
-    if _clang() is None:
+    if clang() is None:
         pytest.skip("clang++ not available")
     with open(KERNELS) as f:
         src = f.read()
@@ -453,38 +291,11 @@ def test_schedule_check_finds_a_missing_barrier(tmp_path):
     emu = Emu(build_emulator(str(tmp_path), str(bad)))
     m, k, n = 3, 4096, 1024
     xb, packed, scale = problem(m, k, n, seed=m)
-    _set_schedule(emu, 0)
+    set_schedule(emu, 0)
     a = run_linear(emu, xb, packed, scale, m, k, n)
-    _set_schedule(emu, 1)
+    set_schedule(emu, 1)
     b = run_linear(emu, xb, packed, scale, m, k, n)
     assert not np.array_equal(a, b)
-
-
-def _place(emu, arr, misalign: int, front: bool) -> int:
-    """Copy arr to a guarded buffer so that its first byte sits `misalign` bytes
-    past a 16-byte boundary.  front=False: the data ends within 16 bytes of the
-    trailing guard page (exactly at it when the sizes allow); front=True: the
-    buffer starts right after the leading guard page."""
-    a = np.ascontiguousarray(arr)
-    if front:
-        emu.lib.emu_alloc_front.restype = ctypes.c_void_p
-        emu.lib.emu_alloc_front.argtypes = [ctypes.c_size_t]
-        p = emu.lib.emu_alloc_front(a.nbytes + misalign) + misalign
-    else:
-        # The buffer ends at a page boundary, so its start is -size (mod 16):
-        # pad the size until the start lands `misalign` past a 16-byte boundary.
-        pad = (-a.nbytes - misalign) % 16
-        p = emu.lib.emu_alloc(a.nbytes + pad)
-    assert p % 16 == misalign % 16
-    ctypes.memmove(p, a.ctypes.data, a.nbytes)
-    return p
-
-
-def _rows_with_stride(rows, cols, ld, dtype, fill):
-    """A [rows, ld] buffer cut right after the last row's `cols` elements."""
-    full = np.zeros((rows, ld), dtype=dtype)
-    full[:, :cols] = fill
-    return full.reshape(-1)[: (rows - 1) * ld + cols]
 
 
 @pytest.mark.parametrize("case", range(24))
@@ -505,11 +316,11 @@ def test_guarded_misaligned_operands(emu, case):
     packed = rng.integers(-128, 128, size=(k // 2, n), dtype=np.int8)
     scale = (rng.random((k // 128, n), dtype=np.float32) * 0.01 + 0.001).astype(np.float32)
     xb = bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
-    xp = _place(emu, _rows_with_stride(m, k, ldx, np.uint16, xb), mx, front)
-    pp = _place(emu, _rows_with_stride(k // 2, n, ldp, np.int8, packed), mp, front)
-    sp = _place(emu, _rows_with_stride(k // 128, n, lds, np.float32, scale), ms, front)
+    xp = place(emu, rows_with_stride(m, k, ldx, np.uint16, xb), mx, front)
+    pp = place(emu, rows_with_stride(k // 2, n, ldp, np.int8, packed), mp, front)
+    sp = place(emu, rows_with_stride(k // 128, n, lds, np.float32, scale), ms, front)
     ylen = (m - 1) * ldy + n
-    yp = _place(emu, np.zeros(ylen, np.uint16), my, front)
+    yp = place(emu, np.zeros(ylen, np.uint16), my, front)
     nb = ctypes.c_size_t(0)
     assert emu.lib.w4a16_workspace_size(m, n, k, 128, ctypes.byref(nb)) == 0
     ws, size = emu.workspace(nb.value)
@@ -519,11 +330,6 @@ def test_guarded_misaligned_operands(emu, case):
     y = np.stack([flat[r * ldy: r * ldy + n] for r in range(m)])
     assert_parity(bf16_value(y).astype(np.float64), orc.fused_reference(bf16_value(xb), packed, scale), desc)
     assert emu.slots_clear(ws, size), desc
-
-
-def _set_concurrency(emu, slots, reverse=False):
-    emu.lib.emu_set_concurrency.argtypes = [ctypes.c_int, ctypes.c_int]
-    emu.lib.emu_set_concurrency(slots, 1 if reverse else 0)
 
 
 # Decode launches with split K: (M, K, N) -> workgroups (strips x splits).
@@ -540,9 +346,9 @@ def test_split_k_with_resident_workgroups(emu, reverse):
     try:
         for m, k, n in SPLIT_K_SHAPES:
             xb, packed, scale = problem(m, k, n, seed=m + k + n, quantized=True)
-            _set_concurrency(emu, 1)
+            set_concurrency(emu, 1)
             seq = run_linear(emu, xb, packed, scale, m, k, n)
-            _set_concurrency(emu, 4096, reverse)
+            set_concurrency(emu, 4096, reverse)
             conc = run_linear(emu, xb, packed, scale, m, k, n)
             assert np.array_equal(seq, conc), f"M={m} K={k} N={n} reverse={reverse}"
         # The SwiGLU pair: every gate workgroup publishes, up's finishers sum both.
@@ -553,7 +359,7 @@ def test_split_k_with_resident_workgroups(emu, reverse):
         assert emu.lib.w4a16_workspace_size_swiglu(m, n, k, 128, ctypes.byref(nb)) == 0
         outs = []
         for slots in (1, 4096):
-            _set_concurrency(emu, slots, reverse and slots > 1)
+            set_concurrency(emu, slots, reverse and slots > 1)
             ws, size = emu.workspace(nb.value)
             h = emu.zeros(m * n * 2)
             assert emu.lib.w4a16_swiglu(emu.put(xb), k, emu.put(gp), n, emu.put(gs), n, emu.put(up), n,
@@ -562,7 +368,7 @@ def test_split_k_with_resident_workgroups(emu, reverse):
             outs.append(emu.get(h, (m, n), np.uint16))
         assert np.array_equal(outs[0], outs[1])
     finally:
-        _set_concurrency(emu, 1)
+        set_concurrency(emu, 1)
 
 
 def test_split_k_give_up_path(emu):
@@ -583,12 +389,12 @@ def test_split_k_give_up_path(emu):
     xp, pp, sp = emu.put(xb), emu.put(packed), emu.put(scale)
     old = lib.w4a16_debug_set_spin_limit(0)
     try:
-        _set_concurrency(emu, 1, reverse=True)
+        set_concurrency(emu, 1, reverse=True)
         y = emu.zeros(m * n * 2)
         assert lib.w4a16_linear(xp, k, pp, n, sp, n, y, n, m, n, k, 128, ws, size, None) == 0
     finally:
         lib.w4a16_debug_set_spin_limit(old)
-        _set_concurrency(emu, 1)
+        set_concurrency(emu, 1)
     out = emu.get(y, (m, n), np.uint16)
     assert (out == 0x7FC0).all()  # every strip's finisher ran before its publishers
     off = ctypes.c_size_t(0)
@@ -607,7 +413,7 @@ def test_kernels_under_undefined_behavior_sanitizer(tmp_path):
     vector access, signed overflow, shifts) on planner-branch shapes, the
     misaligned-operand cases and every other entry point, in a child process
     so that a finding (which aborts) fails this test with its report."""
-    if _clang() is None or _ubsan_runtime() is None:
+    if clang() is None or ubsan_runtime() is None:
         pytest.skip("clang++ with the UBSan runtime not available")
     lib = build_emulator(str(tmp_path), ubsan=True)
     script = textwrap.dedent(f"""
@@ -632,7 +438,6 @@ def test_kernels_under_undefined_behavior_sanitizer(tmp_path):
     """)
     res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=900)
     assert res.returncode == 0 and "ubsan clean" in res.stdout, res.stdout[-2000:] + res.stderr[-4000:]
-
 
 
 @pytest.fixture
