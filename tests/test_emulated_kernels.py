@@ -24,7 +24,10 @@ CPU.  These tests check, with no GPU:
 * the decode split-K protocol with every workgroup resident and interleaved,
   dispatched first-to-last and last-to-first (finishers then poll while their
   publishers run): identical bits, empty slots; and its give-up path, forced
-  with a zero poll budget and finishers dispatched before their publishers.
+  with a zero poll budget and finishers dispatched before their publishers;
+* the kernel code under UndefinedBehaviorSanitizer (alignment of every vector
+  access, signed overflow, shifts);
+* the Python wrappers' operand marshalling, driven with CPU tensors.
 
 What the emulator does not model (timing, caches and the store-to-load
 ordering they allow between workgroups, the matrix cores' rounding order) is
