@@ -205,9 +205,11 @@ def test_dequant_bit_exact(emu):
 
 
 def test_noalloc_matches_linear(emu):
-    """The allocation-free entry point (its scratch is the emulated static array), two calls in a
-    row, the second smaller, against w4a16_linear."""
-    for m, k, n in ((4, 4096, 2048), (2, 1024, 512), (96, 512, 256)):
+    """The allocation-free entry point (its scratch is the emulated static array): calls in a
+    row, smaller after larger and decode after GEMM, against w4a16_linear."""
+    # A decode call after the GEMM: the GEMM's scratch (upper half) must leave the
+    # decode slots (lower half) empty.
+    for m, k, n in ((4, 4096, 2048), (2, 1024, 512), (96, 512, 256), (3, 4096, 1024)):
         xb, packed, scale = problem(m, k, n, seed=m + 1)
         ref = run_linear(emu, xb, packed, scale, m, k, n)
         y = emu.zeros(m * n * 2)
