@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 6
+#define W4A16_ABI_VERSION 7
 
 /* Most problems one grouped call accepts. */
 #define W4A16_MAX_PROBLEMS 16
@@ -41,6 +41,8 @@ extern "C" {
 #define W4A16_ERR_DTYPE 7       /* unknown dtype code */
 #define W4A16_ERR_TOO_LARGE 8   /* problem exceeds what the entry point supports (w4a16_bf16_gemv: M > 16;
                                    decode-sized M whose split-K partials, nsplit * M * N * 4 bytes, reach 4 GB) */
+#define W4A16_ERR_CAPTURING 9   /* the stream is capturing a graph and the call needs eager work first
+                                   (w4a16_linear_noalloc before its scratch is set up; w4a16_noalloc_status) */
 
 /* Bits of a workspace's status word (see w4a16_status_offset). */
 #define W4A16_STATUS_SPLITK_TIMEOUT 1u  /* a decode split-K finisher gave up polling: its outputs are NaN and
@@ -121,12 +123,18 @@ int w4a16_linear(const void* x, int64_t ldx,
  * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
  * the reference.  Same arguments (minus the workspace), arithmetic, results
  * and status codes as w4a16_linear.  Its scratch is a fixed 96 MiB array in
- * the library's own device memory, one per GPU, held until the process ends;
- * the first call on a device looks up its address and zeroes it on `stream`.
- * Calls whose split-K scratch (w4a16_workspace_size) exceeds 96 MiB return
- * W4A16_ERR_TOO_LARGE before anything is launched.  The call itself never
- * allocates.  Every call on one GPU shares that GPU's array: calls that
- * overlap on one GPU (other streams or threads) race, so order them.
+ * the library's own device memory, one per GPU, held until the process ends.
+ * The first call on a device that needs the scratch sets it up: it looks up
+ * the array's address, zeroes it on `stream` and waits for that fill.  That
+ * first call must be eager: made while `stream` is capturing a graph it
+ * returns W4A16_ERR_CAPTURING and launches nothing (make one eager call, or
+ * call w4a16_noalloc_status, on the device first).  Calls whose split-K
+ * scratch (w4a16_workspace_size) exceeds 96 MiB return W4A16_ERR_TOO_LARGE
+ * before anything is launched.  The call itself never allocates.  Every call
+ * on one GPU shares that GPU's array, which keeps the last call's contents:
+ * calls that overlap on one GPU (other streams or threads) race, so order
+ * them.  A split-K give-up (W4A16_STATUS_SPLITK_TIMEOUT) is reported and
+ * cleared by w4a16_noalloc_status.
  */
 int w4a16_linear_noalloc(const void* x, int64_t ldx,
                          const int8_t* packed, int64_t ldp,
@@ -134,6 +142,31 @@ int w4a16_linear_noalloc(const void* x, int64_t ldx,
                          void* y, int64_t ldy,
                          int M, int N, int K, int group_size,
                          void* stream);
+
+/*
+ * Status word of the current device's no-alloc scratch (W4A16_STATUS_*), for
+ * w4a16_linear_noalloc as w4a16_status_offset is for a workspace.  No
+ * counterpart in the reference, whose kernel has no cross-workgroup protocol;
+ * it is for the callers of w4a16_linear_noalloc, which cannot allocate.
+ * Synchronises `stream`, reads the word and, when it is set (a finisher gave
+ * up and late partials may sit in the slots), zeroes the whole scratch on
+ * `stream` and waits for it, so later calls start from empty slots.  Sets the
+ * scratch up if no call has yet.  Refused while `stream` is capturing
+ * (W4A16_ERR_CAPTURING).  Allocates nothing; do not overlap it with
+ * w4a16_linear_noalloc calls on the same GPU.
+ */
+int w4a16_noalloc_status(void* stream, uint32_t* status);
+
+/*
+ * Identity of the graph capture `stream` is in: a non-zero id unique to that
+ * capture, or 0 when the stream is not capturing.  No counterpart in the
+ * reference.  Host bookkeeping for callers that keep one workspace per
+ * stream: a workspace first allocated inside a capture is zeroed by a fill
+ * that only that graph holds, so every other capture that uses it must record
+ * a fill of its own (once per capture) for its replays not to depend on which
+ * graph has replayed first.
+ */
+int w4a16_capture_id(void* stream, unsigned long long* id);
 
 /*
  * Several independent projections: up to W4A16_MAX_PROBLEMS problems, each

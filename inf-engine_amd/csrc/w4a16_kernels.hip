@@ -135,7 +135,9 @@ __device__ __forceinline__ void sum_slots(__amdgpu_buffer_rsrc_t rs, int nslots,
 #pragma unroll
         for (int i = 0; i < SCH; ++i) missing = missing | empty(j, i);  // bitwise: no short-circuit branches
       if (__builtin_amdgcn_ballot_w64(missing) == 0) break;
-      if (spins >= limit) {
+      // After a give-up the later chunks take what has arrived without
+      // waiting, so a give-up costs one poll budget, not one per chunk.
+      if (timed_out || spins >= limit) {
         timed_out = true;
         break;
       }
@@ -1864,17 +1866,36 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(u32x4_t* __restrict__ p,
     p[i] = u32x4_t{0u, 0u, 0u, 0u};
 }
 
-// Device address of the current device's scratch; set up (address lookup and
-// a zero fill on `s`) on the first call on that device.
-int scratch_for_current_device(hipStream_t s, void** out) {
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone;
+}
+
+// Zero the whole scratch on `s` and wait for it.
+int zero_scratch(void* p, hipStream_t s) {
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(1024), dim3(256), 0, s, static_cast<u32x4_t*>(p), kScratchBytes / 16);
+  if (hipGetLastError() != hipSuccess) return W4A16_ERR_LAUNCH;
+  return hipStreamSynchronize(s) == hipSuccess ? W4A16_OK : W4A16_ERR_LAUNCH;
+}
+
+// Device address of the current device's scratch, or null (with W4A16_OK)
+// when it has not been set up and `setup` is false.  Set-up is eager work: the
+// address lookup and a zero fill on `s` that completes before the pointer is
+// published, so a set-up scratch is zero for every stream.  Under graph
+// capture that fill would become a node that re-zeroes 96 MiB on every
+// replay, so a stream that is capturing is refused (W4A16_ERR_CAPTURING): one
+// eager call (or w4a16_noalloc_status) on the device sets the scratch up.
+int scratch_for_current_device(hipStream_t s, bool setup, void** out) {
+  *out = nullptr;
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return W4A16_ERR_LAUNCH;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
+  if (!g_scratch_ptr[dev] && setup) {
+    if (capturing(s)) return W4A16_ERR_CAPTURING;
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return W4A16_ERR_LAUNCH;
-    hipLaunchKernelGGL(fill_zero_kernel, dim3(1024), dim3(256), 0, s, static_cast<u32x4_t*>(p), kScratchBytes / 16);
-    if (hipGetLastError() != hipSuccess) return W4A16_ERR_LAUNCH;
+    const int rc = zero_scratch(p, s);
+    if (rc != W4A16_OK) return rc;
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -1902,6 +1923,9 @@ const char* w4a16_error_string(int code) {
     case W4A16_ERR_LAUNCH: return "HIP kernel launch failed";
     case W4A16_ERR_DTYPE: return "unsupported dtype code";
     case W4A16_ERR_TOO_LARGE: return "problem exceeds the supported size";
+    case W4A16_ERR_CAPTURING:
+      return "the stream is capturing a graph and the call needs eager work first (set up the no-alloc scratch with "
+             "one eager call or w4a16_noalloc_status)";
     default: return "unknown w4a16 error";
   }
 }
@@ -1973,9 +1997,39 @@ int w4a16_linear_noalloc(const void* x, int64_t ldx, const int8_t* packed, int64
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (need == 0) return run(&q, 1, nullptr, 0, s);
   void* ws = nullptr;
-  rc = scratch_for_current_device(s, &ws);
+  rc = scratch_for_current_device(s, true, &ws);
   if (rc != W4A16_OK) return rc;
   return run(&q, 1, ws, kScratchBytes, s);
+}
+
+int w4a16_capture_id(void* stream, unsigned long long* id) {
+  if (!id) return W4A16_ERR_NULL;
+  *id = 0;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  unsigned long long cid = 0;
+  if (hipStreamGetCaptureInfo(static_cast<hipStream_t>(stream), &st, &cid) != hipSuccess) return W4A16_ERR_LAUNCH;
+  if (st == hipStreamCaptureStatusActive) *id = cid;
+  return W4A16_OK;
+}
+
+int w4a16_noalloc_status(void* stream, uint32_t* status) {
+  if (!status) return W4A16_ERR_NULL;
+  *status = 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (capturing(s)) return W4A16_ERR_CAPTURING;
+  void* ws = nullptr;
+  int rc = scratch_for_current_device(s, true, &ws);
+  if (rc != W4A16_OK) return rc;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (hipStreamSynchronize(s) != hipSuccess) return W4A16_ERR_LAUNCH;
+  size_t off = 0;
+  w4a16_status_offset(kScratchBytes, &off);
+  uint32_t word = 0;
+  if (hipMemcpy(&word, static_cast<uint8_t*>(ws) + off, 4, hipMemcpyDeviceToHost) != hipSuccess) return W4A16_ERR_LAUNCH;
+  // A give-up leaves late partials in the slot half: zero it all again.
+  if (word) rc = zero_scratch(ws, s);
+  *status = word;
+  return rc;
 }
 
 int w4a16_workspace_size_swiglu(int M, int N, int K, int group_size, size_t* bytes) {

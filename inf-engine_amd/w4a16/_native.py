@@ -25,11 +25,12 @@ W4A16_ERR_WORKSPACE = 5
 W4A16_ERR_LAUNCH = 6
 W4A16_ERR_DTYPE = 7
 W4A16_ERR_TOO_LARGE = 8
+W4A16_ERR_CAPTURING = 9
 
 W4A16_STATUS_SPLITK_TIMEOUT = 1
 
 # W4A16_ABI_VERSION of include/w4a16.h this binding is written against.
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -51,6 +52,8 @@ EXPORTED_SYMBOLS = (
     "w4a16_status_offset",
     "w4a16_debug_set_spin_limit",
     "w4a16_linear_noalloc",
+    "w4a16_noalloc_status",
+    "w4a16_capture_id",
 )
 
 
@@ -108,6 +111,10 @@ def load_library() -> ctypes.CDLL:
         lib.w4a16_linear.restype = i32
         lib.w4a16_linear_noalloc.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
         lib.w4a16_linear_noalloc.restype = i32
+        lib.w4a16_noalloc_status.argtypes = [vp, ctypes.POINTER(ctypes.c_uint32)]
+        lib.w4a16_noalloc_status.restype = i32
+        lib.w4a16_capture_id.argtypes = [vp, ctypes.POINTER(ctypes.c_ulonglong)]
+        lib.w4a16_capture_id.restype = i32
         lib.w4a16_dequant.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, i32, i32, vp]
         lib.w4a16_dequant.restype = i32
         lib.w4a16_swiglu.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64,
@@ -192,16 +199,19 @@ def workspace_size(m: int, n: int, k: int, group_size: int = 128) -> int:
 # first needs a workspace while it is capturing (torch.cuda.graph captures on
 # its own side stream after the caller warmed up on another one) gets a buffer
 # allocated inside the capture, from the graph's memory pool; its zero fill is
-# a fill kernel recorded into the graph, so every replay starts from empty
-# slots.  Until a replay has run, such a buffer holds no defined data, so an
-# eager call on that stream first zeroes it.
+# a fill kernel recorded into that graph.  Until such a buffer has been zeroed
+# eagerly its contents are defined only inside graphs that hold a fill of it,
+# so every capture that uses it records one fill of its own (once per capture,
+# by capture id) and an eager call zeroes it first.  Replays then never depend
+# on which graph ran first.
 class _Workspace:
-    __slots__ = ("tensor", "captured", "defined")
+    __slots__ = ("tensor", "captured", "defined", "filled_in")
 
-    def __init__(self, tensor: torch.Tensor, captured: bool, defined: bool):
+    def __init__(self, tensor: torch.Tensor, captured: bool, defined: bool, filled_in: set[int]):
         self.tensor = tensor
-        self.captured = captured   # some captured graph holds this buffer's address
-        self.defined = defined     # contents are known to be zero / valid for eager use
+        self.captured = captured    # some captured graph holds this buffer's address
+        self.defined = defined      # zeroed eagerly: every call leaves its slots empty from then on
+        self.filled_in = filled_in  # ids of the captures that recorded a zero fill of this buffer
 
 
 _workspaces: dict[tuple[int, int], _Workspace] = {}
@@ -214,17 +224,28 @@ def _device_index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
 
 
+def capture_id(stream_handle: int) -> int:
+    """Id of the graph capture the stream is in (0 when it is not capturing)."""
+    out = ctypes.c_ulonglong(0)
+    check(load_library().w4a16_capture_id(stream_handle, ctypes.byref(out)), "w4a16_capture_id")
+    return int(out.value)
+
+
 def get_workspace(device: torch.device, stream_handle: int, nbytes: int) -> torch.Tensor | None:
     """The workspace of (device, stream), at least ``nbytes`` long (None for 0)."""
     if nbytes == 0:
         return None
     key = (_device_index(device), stream_handle)
     capturing = torch.cuda.is_current_stream_capturing()
+    cid = capture_id(stream_handle) if capturing else 0
     with _ws_lock:
         ws = _workspaces.get(key)
         if ws is not None and ws.tensor.numel() >= nbytes:
             if capturing:
                 ws.captured = True
+                if not ws.defined and cid not in ws.filled_in:
+                    ws.tensor.zero_()  # recorded into this capture
+                    ws.filled_in.add(cid)
             elif not ws.defined:
                 ws.tensor.zero_()
                 ws.defined = True
@@ -235,7 +256,7 @@ def get_workspace(device: torch.device, stream_handle: int, nbytes: int) -> torc
             if ws.captured:
                 _retired.append(ws.tensor)
         ws = _Workspace(torch.zeros(size, dtype=torch.uint8, device=device), captured=capturing,
-                        defined=not capturing)
+                        defined=not capturing, filled_in={cid} if capturing else set())
         _workspaces[key] = ws
         return ws.tensor
 
@@ -315,17 +336,44 @@ def linear(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_siz
 def linear_noalloc(a: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, y: torch.Tensor,
                    group_size: int = 128) -> None:
     """y = a @ dequant(packed, scale) through w4a16_linear_noalloc, into the
-    caller's y (bf16 [M, N]); no workspace, no allocation in the call."""
+    caller's y (bf16 [M, N], unit column stride, on a's device); no workspace.
+
+    The C call allocates nothing.  Like ``linear``, activations whose rows are
+    not 16-byte aligned are copied when M > 32 (the one allocation here, made
+    before the call; pass aligned rows to avoid it)."""
     lib = load_library()
     m, k = a.shape
     n = packed.shape[1]
-    a, ldx = _rows(a)
+    if (y.dtype != torch.bfloat16 or tuple(y.shape) != (m, n) or (n > 1 and y.stride(1) != 1)
+            or (m > 1 and y.stride(0) < n)):
+        raise ValueError(f"y must be bf16 [{m}, {n}] with unit column stride and disjoint rows, got {y.dtype} "
+                         f"{tuple(y.shape)} strides {tuple(y.stride())}")
+    if y.device != a.device:
+        raise ValueError(f"y is on {y.device}, the activations on {a.device}")
+    a, ldx = _activations(a)
     packed, ldp = _rows(packed)
     scale, lds = _rows(scale)
-    stream = torch.cuda.current_stream(a.device).cuda_stream
-    rc = lib.w4a16_linear_noalloc(a.data_ptr(), ldx, packed.data_ptr(), ldp, scale.data_ptr(), lds,
-                                  y.data_ptr(), y.stride(0), m, n, k, group_size, stream)
+    ldy = y.stride(0) if m > 1 else max(y.stride(0), n)
+    with torch.cuda.device(a.device):
+        stream = torch.cuda.current_stream(a.device).cuda_stream
+        rc = lib.w4a16_linear_noalloc(a.data_ptr(), ldx, packed.data_ptr(), ldp, scale.data_ptr(), lds,
+                                      y.data_ptr(), ldy, m, n, k, group_size, stream)
     check(rc, "w4a16_linear_noalloc")
+
+
+def noalloc_status(device=None) -> int:
+    """Status word of the no-alloc scratch of ``device`` (default: current).
+
+    Synchronises the current stream of that device.  A set
+    W4A16_STATUS_SPLITK_TIMEOUT means a decode finisher gave up and wrote NaN;
+    the scratch is zeroed again before this returns, so later calls start from
+    empty slots.  Sets the scratch up on first use; not allowed under capture."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    out = ctypes.c_uint32(0)
+    with torch.cuda.device(dev):
+        rc = load_library().w4a16_noalloc_status(torch.cuda.current_stream(dev).cuda_stream, ctypes.byref(out))
+    check(rc, "w4a16_noalloc_status")
+    return int(out.value)
 
 
 def linear_grouped(xs, weights, group_size: int) -> list[torch.Tensor]:

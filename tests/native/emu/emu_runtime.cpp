@@ -404,6 +404,10 @@ float shfl_xor(float v, int mask, int width) {
   return collective(kShfl, p).f;
 }
 
+void range_ambiguous() {
+  fail("buffer access in range by one reading of the range check and out of range by another (soffset counted or not, straddling num_records, or a 32-bit offset wrap)");
+}
+
 void vm_issue() { ++g_cur->vm_issued; }
 
 void vm_copy_to_lds(void* dst, const void* src, int bytes) {
@@ -484,6 +488,11 @@ void launch(const char* name, dim3 grid, dim3 block, size_t dyn, const std::func
 }  // namespace emu
 
 // Scheduling order of the threads of a workgroup (see g_schedule).
+namespace emu {
+int g_capturing = 0;
+}
+extern "C" void emu_set_capturing(int on) { emu::g_capturing = on; }
+
 extern "C" void emu_set_schedule(int mode, uint64_t seed) {
   g_schedule = mode;
   g_sched_state = seed * 2 + 1;

@@ -93,12 +93,31 @@ void waitcnt(int code);
 
 inline emu_rsrc make_rsrc(const void* p, short, int num, int) { return emu_rsrc{static_cast<const char*>(p), (uint32_t)num}; }
 
+// Stops the run: a buffer access whose outcome depends on a detail of the
+// hardware's range check (emu_runtime.cpp).
+[[noreturn]] void range_ambiguous();
+
+// The kernels must not depend on two details of the raw-buffer range check
+// that the emulated rule below fixes one way: whether the scalar offset
+// (soffset) counts towards the check or only moves the address, and whether a
+// multi-dword access that straddles num_records is checked per dword or as a
+// whole.  Every access must therefore lie wholly in range or wholly out of
+// range whichever way those are read, with no 32-bit wrap of the offset.
+inline void range_rules_agree(emu_rsrc r, uint64_t vimm, uint32_t soff, int bytes) {
+  const uint64_t full = vimm + soff;
+  if (full >= (1ull << 32)) range_ambiguous();
+  const bool in_v = vimm + bytes <= r.num, out_v = vimm >= r.num;
+  const bool in_full = full + bytes <= r.num, out_full = full >= r.num;
+  if (!((in_v && in_full) || (out_v && out_full))) range_ambiguous();
+}
+
 // Raw buffer rule: each dword (or the one 16-bit word) is in range when its
 // last byte lies below num_records; out-of-range loads read zero and
 // out-of-range stores are dropped.
 template <int BYTES>
 inline void buffer_load(emu_rsrc r, uint32_t voff, uint32_t soff, void* out) {
   vm_issue();
+  range_rules_agree(r, voff, soff, BYTES);
   const uint64_t off = (uint64_t)voff + soff;
   const int unit = BYTES < 4 ? BYTES : 4;
   for (int i = 0; i < BYTES; i += unit) {
@@ -111,6 +130,7 @@ inline void buffer_load(emu_rsrc r, uint32_t voff, uint32_t soff, void* out) {
 template <int BYTES>
 inline void buffer_store(emu_rsrc r, uint32_t voff, uint32_t soff, const void* in) {
   vm_issue();
+  range_rules_agree(r, voff, soff, BYTES);
   const uint64_t off = (uint64_t)voff + soff;
   for (int i = 0; i < BYTES; i += 4)
     if (off + i + 4 <= r.num) memcpy(const_cast<char*>(r.base) + off + i, static_cast<const char*>(in) + i, 4);
@@ -126,6 +146,7 @@ inline void store_b64(emu_u32x2 x, emu_rsrc r, uint32_t v, uint32_t s, int) { bu
 inline void load_lds(emu_rsrc r, void* lds, int size, uint32_t v, uint32_t s, int imm, int) {
   char* dst = static_cast<char*>(lds) + imm + lane_id() * size;
   char data[16];
+  range_rules_agree(r, (uint64_t)v + imm, s, size);
   const uint64_t off = (uint64_t)v + imm + s;
   if (size != 16 && size != 4 && size != 2) __builtin_trap();
   const int unit = size < 4 ? size : 4;
@@ -214,3 +235,20 @@ inline T atomic_load(const T* p) { return *p; }
 inline hipError_t hipGetLastError() { return emu::last_error(); }
 inline hipError_t hipGetDevice(int* d) { *d = 0; return hipSuccess; }
 inline hipError_t hipGetSymbolAddress(void** p, const void* sym) { *p = const_cast<void*>(sym); return hipSuccess; }
+// Stream capture, as the host sees it: emu_set_capturing (emu_runtime.cpp)
+// makes every stream report that it is capturing a graph.
+enum hipStreamCaptureStatus { hipStreamCaptureStatusNone = 0, hipStreamCaptureStatusActive = 1 };
+namespace emu { extern int g_capturing; }
+inline hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus* st) {
+  *st = emu::g_capturing ? hipStreamCaptureStatusActive : hipStreamCaptureStatusNone;
+  return hipSuccess;
+}
+inline hipError_t hipStreamGetCaptureInfo(hipStream_t, hipStreamCaptureStatus* st, unsigned long long* id) {
+  *st = emu::g_capturing ? hipStreamCaptureStatusActive : hipStreamCaptureStatusNone;
+  *id = emu::g_capturing ? (unsigned long long)emu::g_capturing : 0ull;
+  return hipSuccess;
+}
+// Launches run to completion when they are made, so a stream is always idle.
+inline hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+enum hipMemcpyKind { hipMemcpyDeviceToHost = 2 };
+inline hipError_t hipMemcpy(void* dst, const void* src, size_t n, hipMemcpyKind) { memcpy(dst, src, n); return hipSuccess; }

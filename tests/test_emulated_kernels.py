@@ -260,6 +260,39 @@ def test_late_lds_copies_are_modelled(tmp_path):
         assert_parity(bf16_value(y).astype(np.float64), reference(xb, packed, scale, m, k, n), "short wait")
 
 
+def test_range_check_reading_is_pinned(tmp_path):
+    """Negative control for the range-check audit: a GEMM whose exhausted weight
+    loads go past the buffer through the scalar offset (group G) rather than the
+    per-lane offset reads zero if the hardware counts the scalar offset in its
+    range check, and memory past the weights if it does not.  The emulator stops
+    such an access, so the shipped kernels (which pass every test above) do not
+    depend on that detail of the check."""
+    if clang() is None:
+        pytest.skip("clang++ not available")
+    with open(KERNELS) as f:
+        src = f.read()
+    shipped = ("    const int g_next = has_next ? g + KW : g;\n"
+               "    const uint32_t wv_next = (has_next || !w_small) ? wvoff : 0x80000000u;\n")
+    assert src.count(shipped) == 1
+    bad = tmp_path / "w4a16_soffset_oob.hip"
+    bad.write_text(src.replace(shipped, "    const int g_next = has_next ? g + KW : G;\n"
+                                        "    const uint32_t wv_next = wvoff;\n"))
+    lib_path = build_emulator(str(tmp_path), str(bad))
+    script = textwrap.dedent(f"""
+        import sys
+        sys.path[:0] = [{ROOT!r}, {os.path.join(ROOT, 'tests')!r}]
+        from emu_harness import Emu, problem, run_linear
+        emu = Emu({lib_path!r})
+        m, k, n = 256, 512, 512
+        xb, packed, scale = problem(m, k, n, seed=3)
+        run_linear(emu, xb, packed, scale, m, k, n)
+        print("no fault")
+    """)
+    res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
+    assert res.returncode == 97, (res.returncode, res.stdout, res.stderr[-2000:])
+    assert "soffset counted or not" in res.stderr and "gemm_kernel" in res.stderr, res.stderr[-2000:]
+
+
 SCHEDULE_SHAPES = [(1, 1024, 512), (3, 4096, 1024), (16, 2048, 512), (24, 1024, 640), (40, 512, 320),
                    (130, 512, 256), (256, 1024, 512), (200, 512, 333)]
 
@@ -411,6 +444,76 @@ def test_split_k_give_up_path(emu):
     assert lib.w4a16_linear(xp, k, pp, n, sp, n, y2, n, m, n, k, 128, ws, size, None) == 0
     assert np.array_equal(emu.get(y2, (m, n), np.uint16), ref)
     assert emu.slots_clear(ws, size)
+
+
+def test_noalloc_give_up_is_reported_and_cleared(emu):
+    """A forced give-up inside w4a16_linear_noalloc leaves NaN outputs, a set status
+    word and late partials in the shared scratch; w4a16_noalloc_status reports the
+    bit once, zeroes the scratch, and the next call is exact again."""
+    lib = emu.lib
+    lib.w4a16_debug_set_spin_limit.argtypes = [ctypes.c_uint32]
+    lib.w4a16_debug_set_spin_limit.restype = ctypes.c_uint32
+    m, k, n = 2, 4096, 512
+    xb, packed, scale = problem(m, k, n, seed=9, quantized=True)
+    ref = run_linear(emu, xb, packed, scale, m, k, n)
+    xp, pp, sp = emu.put(xb), emu.put(packed), emu.put(scale)
+    st = ctypes.c_uint32(7)
+    assert lib.w4a16_noalloc_status(None, ctypes.byref(st)) == 0 and st.value == 0
+    old = lib.w4a16_debug_set_spin_limit(0)
+    try:
+        set_concurrency(emu, 1, reverse=True)
+        y = emu.zeros(m * n * 2)
+        assert lib.w4a16_linear_noalloc(xp, k, pp, n, sp, n, y, n, m, n, k, 128, None) == 0
+    finally:
+        lib.w4a16_debug_set_spin_limit(old)
+        set_concurrency(emu, 1)
+    assert (emu.get(y, (m, n), np.uint16) == 0x7FC0).all()
+    # Without the reset the late partials would be summed into the next call.
+    assert lib.w4a16_noalloc_status(None, ctypes.byref(st)) == 0 and st.value == 1
+    assert lib.w4a16_noalloc_status(None, ctypes.byref(st)) == 0 and st.value == 0
+    for _ in range(2):
+        y2 = emu.zeros(m * n * 2)
+        assert lib.w4a16_linear_noalloc(xp, k, pp, n, sp, n, y2, n, m, n, k, 128, None) == 0
+        assert np.array_equal(emu.get(y2, (m, n), np.uint16), ref)
+    assert lib.w4a16_noalloc_status(None, ctypes.byref(st)) == 0 and st.value == 0
+
+
+def test_noalloc_first_call_under_capture_is_refused(tmp_path, emu):
+    """In a fresh process, a first no-alloc call made while the stream captures a
+    graph returns W4A16_ERR_CAPTURING and launches nothing (its zero fill would
+    become a 96 MiB node of the graph); after one eager call, calls under capture
+    go through.  The status reader is refused under capture too."""
+    lib_path = emu.lib._name
+    script = textwrap.dedent(f"""
+        import ctypes, sys
+        import numpy as np
+        sys.path[:0] = [{ROOT!r}, {os.path.join(ROOT, 'tests')!r}]
+        from emu_harness import Emu, problem, run_linear
+        emu = Emu({lib_path!r})
+        lib = emu.lib
+        m, k, n = 1, 4096, 512
+        xb, packed, scale = problem(m, k, n, seed=4, quantized=True)
+        ref = run_linear(emu, xb, packed, scale, m, k, n)
+        args = lambda y: (emu.put(xb), k, emu.put(packed), n, emu.put(scale), n, y, n, m, n, k, 128, None)
+        st = ctypes.c_uint32(0)
+        lib.emu_set_capturing(1)
+        y = emu.zeros(m * n * 2)
+        assert lib.w4a16_linear_noalloc(*args(y)) == 9
+        assert not emu.get(y, (m, n), np.uint16).any()
+        assert lib.w4a16_noalloc_status(None, ctypes.byref(st)) == 9
+        lib.emu_set_capturing(0)
+        assert lib.w4a16_linear_noalloc(*args(y)) == 0
+        assert np.array_equal(emu.get(y, (m, n), np.uint16), ref)
+        lib.emu_set_capturing(1)
+        y = emu.zeros(m * n * 2)
+        assert lib.w4a16_linear_noalloc(*args(y)) == 0
+        assert np.array_equal(emu.get(y, (m, n), np.uint16), ref)
+        lib.emu_set_capturing(0)
+        assert lib.w4a16_noalloc_status(None, ctypes.byref(st)) == 0 and st.value == 0
+        print("capture rule ok")
+    """)
+    res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0 and "capture rule ok" in res.stdout, res.stdout[-2000:] + res.stderr[-3000:]
 
 
 def test_kernels_under_undefined_behavior_sanitizer(tmp_path):

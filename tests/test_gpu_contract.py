@@ -173,6 +173,40 @@ def test_device_quantize_ties_and_amax():
     assert orc.codes(p.cpu().numpy())[:8, 0].tolist() == [7, 0, 2, 2, 0, -2, -2, 4]
 
 
+def test_capture_born_workspace_replays_in_any_order():
+    """Two decode buckets captured one after the other on a fresh stream, so the
+    stream's workspace is born inside the first capture and reused by the second.
+    The buffer is then poisoned and the second graph replayed before the first has
+    ever run: its own recorded fill must give outputs bit-equal to eager."""
+    from w4a16 import _native, int4_matmul, synth
+
+    packed, scale = synth.make_weight(4096, 12288, seed=41, device=DEV)
+    xs = {m: synth.make_activations(m, 4096, seed=42 + m, device=DEV) for m in (1, 4)}
+    eager = {m: int4_matmul(xs[m], packed, scale) for m in xs}
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    graphs = {}
+    for m in (4, 1):  # the larger need first, so the second capture reuses the buffer
+        say(f"capture-born workspace: capture M={m}")
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            out = int4_matmul(xs[m], packed, scale)
+        graphs[m] = (g, out)
+    ws = _native._workspaces[(torch.device(DEV).index or 0, s.cuda_stream)]
+    assert ws.captured and not ws.defined and len(ws.filled_in) == 2
+    for order in ((1, 4), (4, 1)):
+        ws.tensor.fill_(0x55)  # what a pool buffer may hold before any fill ran
+        torch.cuda.synchronize()
+        for m in order:
+            g, out = graphs[m]
+            out.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager[m]), f"replay order {order}, M={m}"
+    assert _native.workspace_status() == 0
+
+
 def test_splitk_give_up_sets_status_and_workspace_recovers():
     """Zero poll budget (host-forced): each finisher either sees every slot on
     its first poll or gives up at once.  Every kernel ends normally.  Columns of

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(native_lib):
     assert set(names) == set(_native.EXPORTED_SYMBOLS), names
     for name in names:
         assert hasattr(native_lib, name), name
-    assert native_lib.w4a16_abi_version() == _native.ABI_VERSION == 6
+    assert native_lib.w4a16_abi_version() == _native.ABI_VERSION == 7
 
 
 def _linear(lib, *, x=1, ldx=4096, packed=1, ldp=4096, scale=1, lds=4096, y=1, ldy=4096, m=1, n=4096,

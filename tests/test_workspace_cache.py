@@ -11,7 +11,13 @@ rules under real captures: tests/test_gpu_contract.py):
 * outgrowing a buffer that no capture used drops it; outgrowing one that a
   capture used keeps it alive for the rest of the process;
 * a buffer first allocated inside a capture is not known to be zero until a
-  replay ran, so the next eager call on that stream zeroes it first.
+  replay ran, so the next eager call on that stream zeroes it first;
+* every other capture that uses such a buffer records a zero fill of its own,
+  once per capture, so no graph's replays depend on another graph having
+  replayed first.
+
+On CPU tensors a "recorded" fill runs at once, which is what makes it visible
+here.
 """
 
 from __future__ import annotations
@@ -27,8 +33,9 @@ DEV = torch.device("cpu", 0)  # any device with an index; the cache never launch
 @pytest.fixture
 def cache(monkeypatch):
     """A fresh cache with a settable 'is capturing' flag."""
-    state = {"capturing": False}
+    state = {"capturing": False, "id": 1}
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: state["capturing"])
+    monkeypatch.setattr(_native, "capture_id", lambda handle: state["id"] if state["capturing"] else 0)
     monkeypatch.setattr(_native, "_workspaces", {})
     monkeypatch.setattr(_native, "_retired", [])
     return state
@@ -90,3 +97,28 @@ def test_capture_of_a_grown_buffer_inside_the_capture(cache):
     assert b is not a and any(t is a for t in _native._retired)
     ws = _native._workspaces[(0, 31)]
     assert ws.captured and not ws.defined
+
+
+def test_each_capture_that_reuses_a_capture_born_buffer_fills_it_once(cache):
+    """The reference captures one graph per decode bucket on torch's capture stream
+    (engine/llama_paged_engine.py:315-347).  A buffer born in the first capture is
+    reused by the next ones; each records its own fill (once), so replaying the
+    second graph before the first has ever run still starts from empty slots."""
+    cache["capturing"], cache["id"] = True, 101
+    a = _native.get_workspace(DEV, 41, 1000)
+    ws = _native._workspaces[(0, 41)]
+    assert ws.filled_in == {101}
+    a.fill_(7)
+    assert _native.get_workspace(DEV, 41, 500) is a and a.eq(7).all()  # same capture: no second fill
+    cache["id"] = 102
+    assert _native.get_workspace(DEV, 41, 1000) is a and not a.any()  # its own fill
+    a.fill_(7)
+    assert _native.get_workspace(DEV, 41, 1000) is a and a.eq(7).all()  # once per capture
+    assert ws.filled_in == {101, 102} and not ws.defined
+    # Once zeroed eagerly the buffer stays zero between calls: later captures record no fill.
+    cache["capturing"] = False
+    assert _native.get_workspace(DEV, 41, 1000) is a and not a.any() and ws.defined
+    cache["capturing"], cache["id"] = True, 103
+    a.fill_(7)
+    assert _native.get_workspace(DEV, 41, 1000) is a and a.eq(7).all()
+    assert ws.filled_in == {101, 102}

@@ -96,3 +96,46 @@ def test_noalloc_captured_in_a_graph(native_lib):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, ref)
+
+
+def test_noalloc_status_reports_and_clears_a_give_up(native_lib):
+    """Host-forced give-ups (zero poll budget) inside w4a16_linear_noalloc: columns
+    of a strip that gave up are NaN and noalloc_status() reports the bit; after it
+    has cleared the scratch, calls are exact again and the status reads zero."""
+    from w4a16 import _native
+
+    x, packed, scale = _case(1, 12288, 4096, seed=61)  # down_proj shape: 24 splits at M=1
+    ref = _native.linear(x, packed, scale, 128)
+    torch.cuda.synchronize()
+    assert _native.noalloc_status() == 0
+    old = _native.set_spin_limit(0)
+    gave_up = 0
+    try:
+        for _ in range(5):
+            y = _noalloc(x, packed, scale)
+            torch.cuda.synchronize()
+            status = _native.noalloc_status()
+            nan = torch.isnan(y.float())
+            assert torch.equal(y[~nan], ref[~nan])
+            if nan.any():
+                assert status & _native.W4A16_STATUS_SPLITK_TIMEOUT
+                gave_up += 1
+            else:
+                assert status == 0
+    finally:
+        _native.set_spin_limit(old)
+    say(f"noalloc give-ups in 5 calls with a zero poll budget: {gave_up}")
+    for _ in range(3):
+        assert torch.equal(_noalloc(x, packed, scale), ref)
+    assert _native.noalloc_status() == 0
+
+
+def test_noalloc_wrapper_validates_y():
+    from w4a16 import _native
+
+    x, packed, scale = _case(2, 1024, 512, seed=3)
+    for y in (torch.empty(2, 512, dtype=torch.float32, device=DEV),
+              torch.empty(2, 256, dtype=torch.bfloat16, device=DEV),
+              torch.empty(512, 2, dtype=torch.bfloat16, device=DEV).t()):
+        with pytest.raises(ValueError):
+            _native.linear_noalloc(x, packed, scale, y)
