@@ -87,6 +87,7 @@ class Emu:
         lib.w4a16_status_offset.argtypes = [sz, ctypes.POINTER(sz)]
         lib.w4a16_noalloc_status.argtypes = [vp, ctypes.POINTER(ctypes.c_uint32)]
         lib.emu_set_capturing.argtypes = [i32]
+        lib.emu_load_count.restype = ctypes.c_uint64
         sys.path.insert(0, os.path.join(ROOT, "inf-engine_amd"))
         from w4a16 import _native
         self.Problem = _native.Problem

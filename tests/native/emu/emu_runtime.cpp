@@ -490,8 +490,12 @@ void launch(const char* name, dim3 grid, dim3 block, size_t dyn, const std::func
 // Scheduling order of the threads of a workgroup (see g_schedule).
 namespace emu {
 int g_capturing = 0;
+uint64_t g_loads = 0;  // fibers run one at a time: no atomics needed
+void count_load() { ++g_loads; }
 }
 extern "C" void emu_set_capturing(int on) { emu::g_capturing = on; }
+extern "C" uint64_t emu_load_count() { return emu::g_loads; }
+extern "C" void emu_reset_load_count() { emu::g_loads = 0; }
 
 extern "C" void emu_set_schedule(int mode, uint64_t seed) {
   g_schedule = mode;

@@ -88,6 +88,7 @@ hipError_t last_error();
 // when a wait (s_waitcnt vmcnt(n)) leaves at most n younger operations
 // outstanding, as on the hardware, where such copies land asynchronously.
 void vm_issue();
+void count_load();  // buffer loads issued since emu_reset_load_count
 void vm_copy_to_lds(void* dst, const void* src, int bytes);
 void waitcnt(int code);
 
@@ -117,6 +118,7 @@ inline void range_rules_agree(emu_rsrc r, uint64_t vimm, uint32_t soff, int byte
 template <int BYTES>
 inline void buffer_load(emu_rsrc r, uint32_t voff, uint32_t soff, void* out) {
   vm_issue();
+  count_load();
   range_rules_agree(r, voff, soff, BYTES);
   const uint64_t off = (uint64_t)voff + soff;
   const int unit = BYTES < 4 ? BYTES : 4;

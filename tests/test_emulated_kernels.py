@@ -516,6 +516,41 @@ def test_noalloc_first_call_under_capture_is_refused(tmp_path, emu):
     assert res.returncode == 0 and "capture rule ok" in res.stdout, res.stdout[-2000:] + res.stderr[-3000:]
 
 
+def test_give_up_costs_one_poll_budget(emu):
+    """A finisher that gives up waits one poll budget in all, not one per chunk of
+    slots: with every finisher dispatched before its publishers, the buffer loads
+    added by raising the budget are the same for 8 published slots (one chunk) as
+    for 17 or 23 (three chunks).  Counted over the whole launch; the slope is
+    4 strips x 64 lanes x 8 polls per round."""
+    lib = emu.lib
+    lib.w4a16_debug_set_spin_limit.argtypes = [ctypes.c_uint32]
+    lib.w4a16_debug_set_spin_limit.restype = ctypes.c_uint32
+    m, n = 1, 256
+    slopes = []
+    old = lib.w4a16_debug_set_spin_limit(0)
+    try:
+        set_concurrency(emu, 1, reverse=True)
+        for k in (4608, 9216, 12288):  # 9, 18 and 24 K splits
+            xb, packed, scale = problem(m, k, n, seed=1, quantized=True)
+            nb = ctypes.c_size_t(0)
+            assert lib.w4a16_workspace_size(m, n, k, 128, ctypes.byref(nb)) == 0
+            loads = []
+            for budget in (0, 100):
+                ws, size = emu.workspace(nb.value)
+                lib.w4a16_debug_set_spin_limit(budget)
+                y = emu.zeros(m * n * 2)
+                lib.emu_reset_load_count()
+                assert lib.w4a16_linear(emu.put(xb), k, emu.put(packed), n, emu.put(scale), n, y, n, m, n, k, 128,
+                                        ws, size, None) == 0
+                loads.append(lib.emu_load_count())
+                assert (emu.get(y, (m, n), np.uint16) == 0x7FC0).all()
+            slopes.append(loads[1] - loads[0])
+    finally:
+        lib.w4a16_debug_set_spin_limit(old)
+        set_concurrency(emu, 1)
+    assert slopes == [4 * 64 * 8 * 100] * 3, slopes
+
+
 def test_kernels_under_undefined_behavior_sanitizer(tmp_path):
     """The kernel code built with UndefinedBehaviorSanitizer (alignment of every
     vector access, signed overflow, shifts) on planner-branch shapes, the
