@@ -671,3 +671,47 @@ def test_wrappers_grouped_swiglu_and_gemv(wrappers_on_emulator):
     y = nat.bf16_gemv(xg_off, w)  # unaligned rows are copied for the GEMV
     ref = xg.double().numpy() @ w.double().numpy().T
     assert_parity(y.float().numpy().astype(np.float64), ref, "bf16_gemv unaligned x")
+
+
+def test_integration_ctypes_stub_runs_on_the_emulator(emu, monkeypatch):
+    """The Option B ctypes stub of INTEGRATION.md, executed as written against the
+    emulated library with CPU tensors: outputs match the oracle, and its workspace
+    bookkeeping follows the capture rule (a buffer born in one capture gets a fill
+    recorded by each other capture that uses it, once; an eager call zeroes it)."""
+    import re
+    from types import SimpleNamespace
+
+    import torch
+
+    with open(os.path.join(ROOT, "INTEGRATION.md")) as f:
+        text = f.read()
+    stub = next(b for b in re.findall(r"```python\n(.*?)```", text, re.S) if "def int4_matmul_device" in b)
+    assert stub.count('"/path/to/libw4a16.so"') == 1
+    stub = stub.replace('"/path/to/libw4a16.so"', repr(emu.lib._name))
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda device=None: SimpleNamespace(cuda_stream=0))
+    ns: dict = {}
+    exec(compile(stub, "INTEGRATION.md", "exec"), ns)
+    for m, k, n in ((1, 4096, 512), (3, 1024, 384), (40, 512, 256)):
+        x, packed, scale = _torch_problem(m, k, n, seed=m)
+        y = ns["int4_matmul_device"](x, packed, scale)
+        assert_parity(y.float().numpy().astype(np.float64), _ref(x, packed, scale), f"stub M={m} K={k} N={n}")
+    # Capture bookkeeping (on the CPU a recorded fill runs at once, which makes it visible).
+    x, packed, scale = _torch_problem(1, 4096, 512, seed=7)
+    ref = _ref(x, packed, scale)
+    ns["_ws"].clear()
+    try:
+        emu.lib.emu_set_capturing(5)
+        ns["int4_matmul_device"](x, packed, scale)
+        entry = ns["_ws"][(None, 0)]
+        assert entry[1] is False and entry[2] == {5}
+        entry[0].fill_(0x55)
+        emu.lib.emu_set_capturing(6)  # another capture reuses the buffer: its own fill first
+        y = ns["int4_matmul_device"](x, packed, scale)
+        assert entry[2] == {5, 6}
+        assert_parity(y.float().numpy().astype(np.float64), ref, "stub, second capture")
+    finally:
+        emu.lib.emu_set_capturing(0)
+    entry[0].fill_(0x55)
+    y = ns["int4_matmul_device"](x, packed, scale)  # eager: zeroed first
+    assert entry[1] is True
+    assert_parity(y.float().numpy().astype(np.float64), ref, "stub, eager after captures")
