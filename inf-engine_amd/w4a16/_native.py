@@ -224,10 +224,13 @@ def _device_index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
 
 
-def capture_id(stream_handle: int) -> int:
-    """Id of the graph capture the stream is in (0 when it is not capturing)."""
+def capture_id(stream_handle: int) -> int | None:
+    """Id of the graph capture the stream is in (0 when it is not capturing),
+    or None when the runtime cannot say (the caller then treats every use as a
+    new capture, which is safe but records more fills)."""
     out = ctypes.c_ulonglong(0)
-    check(load_library().w4a16_capture_id(stream_handle, ctypes.byref(out)), "w4a16_capture_id")
+    if load_library().w4a16_capture_id(stream_handle, ctypes.byref(out)) != W4A16_OK:
+        return None
     return int(out.value)
 
 
@@ -243,7 +246,7 @@ def get_workspace(device: torch.device, stream_handle: int, nbytes: int) -> torc
         if ws is not None and ws.tensor.numel() >= nbytes:
             if capturing:
                 ws.captured = True
-                if not ws.defined and cid not in ws.filled_in:
+                if not ws.defined and (cid is None or cid not in ws.filled_in):
                     ws.tensor.zero_()  # recorded into this capture
                     ws.filled_in.add(cid)
             elif not ws.defined:

@@ -122,3 +122,14 @@ def test_each_capture_that_reuses_a_capture_born_buffer_fills_it_once(cache):
     a.fill_(7)
     assert _native.get_workspace(DEV, 41, 1000) is a and a.eq(7).all()
     assert ws.filled_in == {101, 102}
+
+
+def test_unknown_capture_id_records_a_fill_on_every_use(cache, monkeypatch):
+    """If the runtime cannot name the capture, every use of a capture-born buffer
+    inside a capture records a fill: more fills, never a missing one."""
+    monkeypatch.setattr(_native, "capture_id", lambda handle: None)
+    cache["capturing"] = True
+    a = _native.get_workspace(DEV, 51, 1000)
+    for _ in range(2):
+        a.fill_(7)
+        assert _native.get_workspace(DEV, 51, 1000) is a and not a.any()
