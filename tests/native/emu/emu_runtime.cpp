@@ -30,6 +30,7 @@
 
 #include <algorithm>
 #include <deque>
+#include <unordered_map>
 #include <vector>
 
 namespace {
@@ -366,6 +367,7 @@ bool run_round(Block& b) {
 }  // namespace
 
 namespace emu {
+extern std::unordered_map<uintptr_t, std::pair<uint64_t, bool>> g_written;  // coherence audit, below
 
 emu_uint3 g_grid_dim{1, 1, 1}, g_block_dim{1, 1, 1};
 
@@ -451,6 +453,7 @@ void launch(const char* name, dim3 grid, dim3 block, size_t dyn, const std::func
     g_error = hipErrorInvalidValue;
     return;
   }
+  g_written.clear();
   g_grid_dim = emu_uint3{grid.x, grid.y, 1};
   g_block_dim = emu_uint3{block.x, 1, 1};
   g_body = &body;
@@ -487,16 +490,40 @@ void launch(const char* name, dim3 grid, dim3 block, size_t dyn, const std::func
 
 }  // namespace emu
 
-// Scheduling order of the threads of a workgroup (see g_schedule).
 namespace emu {
 int g_capturing = 0;
 uint64_t g_loads = 0;  // fibers run one at a time: no atomics needed
 void count_load() { ++g_loads; }
+
+// Coherence audit: dword address -> (writing workgroup + 1, store was
+// agent-coherent), for the current launch only (reset by launch()).
+constexpr int kCoherentBit = 16;
+std::unordered_map<uintptr_t, std::pair<uint64_t, bool>> g_written;
+uint64_t cur_block_id() {
+  const Block* b = g_cur ? g_cur->blk : nullptr;
+  return b ? (uint64_t)b->bid.y * g_grid_dim.x + b->bid.x + 1 : 0;
 }
+void note_store(const char* p, int bytes, int aux) {
+  for (int i = 0; i < bytes; i += 4)
+    g_written[(uintptr_t)(p + i) & ~(uintptr_t)3] = {cur_block_id(), (aux & kCoherentBit) != 0};
+}
+void check_load(const char* p, int bytes, int aux) {
+  if (g_written.empty()) return;
+  for (int i = 0; i < bytes; i += 4) {
+    const auto it = g_written.find((uintptr_t)(p + i) & ~(uintptr_t)3);
+    if (it == g_written.end() || it->second.first == cur_block_id()) continue;
+    if (!(aux & kCoherentBit) || !it->second.second)
+      fail("a workgroup read data another workgroup stored in the same launch without agent-coherent accesses on "
+           "both sides (on the chip the load can hit a stale line of its own cache)");
+  }
+}
+}  // namespace emu
+
 extern "C" void emu_set_capturing(int on) { emu::g_capturing = on; }
 extern "C" uint64_t emu_load_count() { return emu::g_loads; }
 extern "C" void emu_reset_load_count() { emu::g_loads = 0; }
 
+// Scheduling order of the threads of a workgroup (see g_schedule).
 extern "C" void emu_set_schedule(int mode, uint64_t seed) {
   g_schedule = mode;
   g_sched_state = seed * 2 + 1;

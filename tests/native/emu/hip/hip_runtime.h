@@ -10,7 +10,10 @@
 // memory access is an ordinary host access, so a kernel that leaves its
 // buffers touches a guard page and is reported (emu_alloc in
 // emu_runtime.cpp).  Direct-to-LDS copies land only when a wait
-// (s_waitcnt vmcnt) covers them, as on the hardware.  Workgroups run one
+// (s_waitcnt vmcnt) covers them, as on the hardware.  Buffer accesses are
+// also audited: their outcome must not depend on how the range check treats
+// the scalar offset, and a load of data another workgroup stored in the same
+// launch must be agent-coherent, as must that store.  Workgroups run one
 // after another in dispatch order, or (decode kernels, emu_set_concurrency)
 // several at once, interleaved at every meeting point.  What this does NOT
 // model: timing, caches and the memory ordering they allow (every store is
@@ -89,6 +92,11 @@ hipError_t last_error();
 // outstanding, as on the hardware, where such copies land asynchronously.
 void vm_issue();
 void count_load();  // buffer loads issued since emu_reset_load_count
+// Cross-workgroup coherence audit (emu_runtime.cpp): within one launch, a
+// buffer load of a dword that another workgroup stored must carry the
+// agent-coherence bit, and so must that store; otherwise the run stops.
+void note_store(const char* p, int bytes, int aux);
+void check_load(const char* p, int bytes, int aux);
 void vm_copy_to_lds(void* dst, const void* src, int bytes);
 void waitcnt(int code);
 
@@ -116,36 +124,41 @@ inline void range_rules_agree(emu_rsrc r, uint64_t vimm, uint32_t soff, int byte
 // last byte lies below num_records; out-of-range loads read zero and
 // out-of-range stores are dropped.
 template <int BYTES>
-inline void buffer_load(emu_rsrc r, uint32_t voff, uint32_t soff, void* out) {
+inline void buffer_load(emu_rsrc r, uint32_t voff, uint32_t soff, void* out, int aux) {
   vm_issue();
   count_load();
   range_rules_agree(r, voff, soff, BYTES);
   const uint64_t off = (uint64_t)voff + soff;
   const int unit = BYTES < 4 ? BYTES : 4;
   for (int i = 0; i < BYTES; i += unit) {
-    if (off + i + unit <= r.num)
+    if (off + i + unit <= r.num) {
+      check_load(r.base + off + i, unit, aux);
       memcpy(static_cast<char*>(out) + i, r.base + off + i, unit);
-    else
+    } else {
       memset(static_cast<char*>(out) + i, 0, unit);
+    }
   }
 }
 template <int BYTES>
-inline void buffer_store(emu_rsrc r, uint32_t voff, uint32_t soff, const void* in) {
+inline void buffer_store(emu_rsrc r, uint32_t voff, uint32_t soff, const void* in, int aux) {
   vm_issue();
   range_rules_agree(r, voff, soff, BYTES);
   const uint64_t off = (uint64_t)voff + soff;
   for (int i = 0; i < BYTES; i += 4)
-    if (off + i + 4 <= r.num) memcpy(const_cast<char*>(r.base) + off + i, static_cast<const char*>(in) + i, 4);
+    if (off + i + 4 <= r.num) {
+      note_store(r.base + off + i, 4, aux);
+      memcpy(const_cast<char*>(r.base) + off + i, static_cast<const char*>(in) + i, 4);
+    }
 }
-inline emu_u32x4 load_b128(emu_rsrc r, uint32_t v, uint32_t s, int) { emu_u32x4 o; buffer_load<16>(r, v, s, &o); return o; }
-inline emu_u32x2 load_b64(emu_rsrc r, uint32_t v, uint32_t s, int) { emu_u32x2 o; buffer_load<8>(r, v, s, &o); return o; }
-inline uint32_t load_b32(emu_rsrc r, uint32_t v, uint32_t s, int) { uint32_t o; buffer_load<4>(r, v, s, &o); return o; }
-inline uint16_t load_b16(emu_rsrc r, uint32_t v, uint32_t s, int) { uint16_t o; buffer_load<2>(r, v, s, &o); return o; }
-inline void store_b32(uint32_t x, emu_rsrc r, uint32_t v, uint32_t s, int) { buffer_store<4>(r, v, s, &x); }
-inline void store_b64(emu_u32x2 x, emu_rsrc r, uint32_t v, uint32_t s, int) { buffer_store<8>(r, v, s, &x); }
+inline emu_u32x4 load_b128(emu_rsrc r, uint32_t v, uint32_t s, int a) { emu_u32x4 o; buffer_load<16>(r, v, s, &o, a); return o; }
+inline emu_u32x2 load_b64(emu_rsrc r, uint32_t v, uint32_t s, int a) { emu_u32x2 o; buffer_load<8>(r, v, s, &o, a); return o; }
+inline uint32_t load_b32(emu_rsrc r, uint32_t v, uint32_t s, int a) { uint32_t o; buffer_load<4>(r, v, s, &o, a); return o; }
+inline uint16_t load_b16(emu_rsrc r, uint32_t v, uint32_t s, int a) { uint16_t o; buffer_load<2>(r, v, s, &o, a); return o; }
+inline void store_b32(uint32_t x, emu_rsrc r, uint32_t v, uint32_t s, int a) { buffer_store<4>(r, v, s, &x, a); }
+inline void store_b64(emu_u32x2 x, emu_rsrc r, uint32_t v, uint32_t s, int a) { buffer_store<8>(r, v, s, &x, a); }
 // Direct-to-LDS load: lane l's `size` bytes go to lds + offset + l * size once
 // a later wait covers the copy (vm_copy_to_lds).
-inline void load_lds(emu_rsrc r, void* lds, int size, uint32_t v, uint32_t s, int imm, int) {
+inline void load_lds(emu_rsrc r, void* lds, int size, uint32_t v, uint32_t s, int imm, int aux) {
   char* dst = static_cast<char*>(lds) + imm + lane_id() * size;
   char data[16];
   range_rules_agree(r, (uint64_t)v + imm, s, size);
@@ -153,10 +166,12 @@ inline void load_lds(emu_rsrc r, void* lds, int size, uint32_t v, uint32_t s, in
   if (size != 16 && size != 4 && size != 2) __builtin_trap();
   const int unit = size < 4 ? size : 4;
   for (int i = 0; i < size; i += unit) {
-    if (off + i + unit <= r.num)
+    if (off + i + unit <= r.num) {
+      check_load(r.base + off + i, unit, aux);
       memcpy(data + i, r.base + off + i, unit);
-    else
+    } else {
       memset(data + i, 0, unit);
+    }
   }
   vm_copy_to_lds(dst, data, size);
 }

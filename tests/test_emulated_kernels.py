@@ -21,6 +21,9 @@ CPU.  These tests check, with no GPU:
 * races inside a workgroup: results must not depend on the order in which the
   emulator runs the threads between meeting points (a decode kernel with its
   reduction barrier removed is the negative control);
+* the raw-buffer range check read both ways (scalar offset counted or not) and
+  cross-workgroup data read only through agent-coherent accesses (negative
+  controls for both);
 * the decode split-K protocol with every workgroup resident and interleaved,
   dispatched first-to-last and last-to-first (finishers then poll while their
   publishers run): identical bits, empty slots; and its give-up path, forced
@@ -291,6 +294,36 @@ def test_range_check_reading_is_pinned(tmp_path):
     res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
     assert res.returncode == 97, (res.returncode, res.stdout, res.stderr[-2000:])
     assert "soffset counted or not" in res.stderr and "gemm_kernel" in res.stderr, res.stderr[-2000:]
+
+
+def test_cross_workgroup_reads_must_be_coherent(tmp_path):
+    """Negative control for the coherence audit: a decode kernel whose split-K
+    finisher polls the published slots with ordinary loads (no agent-coherence
+    bit) could read a stale line of its own cache on the chip; the emulator,
+    where every store is visible at once, stops it.  The shipped kernels pass
+    the whole suite with the audit on."""
+    if clang() is None:
+        pytest.skip("clang++ not available")
+    with open(KERNELS) as f:
+        src = f.read()
+    poll = "raw_buffer_load_b32(rs, off[j] + (uint32_t)(sp0 + i) * stride, 0, kAgentCoherent)"
+    assert src.count(poll) == 2
+    bad = tmp_path / "w4a16_plain_polls.hip"
+    bad.write_text(src.replace(poll, poll.replace("kAgentCoherent", "0")))
+    lib_path = build_emulator(str(tmp_path), str(bad))
+    script = textwrap.dedent(f"""
+        import sys
+        sys.path[:0] = [{ROOT!r}, {os.path.join(ROOT, 'tests')!r}]
+        from emu_harness import Emu, problem, run_linear
+        emu = Emu({lib_path!r})
+        m, k, n = 1, 4096, 512
+        xb, packed, scale = problem(m, k, n, seed=3)
+        run_linear(emu, xb, packed, scale, m, k, n)
+        print("no fault")
+    """)
+    res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
+    assert res.returncode == 97, (res.returncode, res.stdout, res.stderr[-2000:])
+    assert "without agent-coherent accesses" in res.stderr and "gemv_kernel" in res.stderr, res.stderr[-2000:]
 
 
 SCHEDULE_SHAPES = [(1, 1024, 512), (3, 4096, 1024), (16, 2048, 512), (24, 1024, 640), (40, 512, 320),
