@@ -38,6 +38,7 @@ namespace {
 constexpr size_t kStackBytes = 128 * 1024;
 constexpr int kMaxThreads = 1024;
 constexpr size_t kMaxDynLds = 160 * 1024;
+constexpr size_t kLdsBytes = 160 * 1024;  // LDS one gfx950 workgroup can hold
 
 enum Coll { kNone = 0, kMfma, kBallot, kFirst, kShfl };
 
@@ -89,6 +90,17 @@ struct Block {
   char* lds = nullptr;
   char* lds_map = nullptr;
   size_t lds_map_bytes = 0;
+  size_t dyn_bytes = 0;
+  // Static LDS objects of the kernel (__shared__ arrays), one guarded,
+  // poisoned allocation each per workgroup.
+  struct StaticLds {
+    int id;
+    char* p;
+    char* map;
+    size_t map_bytes, bytes;
+  };
+  std::vector<StaticLds> statics;
+  size_t static_bytes = 0;
 };
 
 std::vector<Lane*> g_free_lanes;
@@ -316,6 +328,7 @@ Block* start_block(emu_uint3 bid, int nt, size_t dyn) {
   Block* b = new Block();
   b->bid = bid;
   b->nt = b->alive = nt;
+  b->dyn_bytes = dyn;
   if (dyn > 0) {
     b->lds = static_cast<char*>(guarded(dyn, &b->lds_map_bytes, &b->lds_map));
     memset(b->lds, 0xA5, dyn);  // LDS starts undefined: make stale reads visible
@@ -341,6 +354,7 @@ Block* start_block(emu_uint3 bid, int nt, size_t dyn) {
 void finish_block(Block* b) {
   for (Lane* L : b->lanes) g_free_lanes.push_back(L);
   if (b->lds_map) munmap(b->lds_map, b->lds_map_bytes);
+  for (auto& st : b->statics) munmap(st.map, st.map_bytes);
   delete b;
 }
 
@@ -375,6 +389,28 @@ const emu_uint3* cur_tid() { return &g_cur->tid; }
 const emu_uint3* cur_bid() { return &g_cur->blk->bid; }
 int lane_id() { return g_cur->tid.x & 63; }
 void* dyn_lds() { return g_cur->blk->lds; }
+
+// The workgroup's static LDS object `id` (one per __shared__ declarator of
+// the source) of `bytes` bytes: allocated, guarded and poisoned on the first
+// thread's call, shared by the workgroup's other threads.  Static plus
+// dynamic LDS must fit the 160 KB a gfx950 workgroup can hold.
+void* static_lds(int id, size_t bytes) {
+  Block* b = g_cur->blk;
+  for (auto& st : b->statics)
+    if (st.id == id) {
+      if (st.bytes != bytes) fail("static LDS object declared with two sizes");
+      return st.p;
+    }
+  Block::StaticLds st{};
+  st.id = id;
+  st.bytes = bytes;
+  st.p = static_cast<char*>(guarded(bytes, &st.map_bytes, &st.map));
+  memset(st.p, 0xA5, bytes);
+  b->statics.push_back(st);
+  b->static_bytes += bytes;
+  if (b->static_bytes + b->dyn_bytes > kLdsBytes) fail("static plus dynamic LDS exceeds 160 KB per workgroup");
+  return st.p;
+}
 hipError_t last_error() {
   const hipError_t e = g_error;
   g_error = hipSuccess;

@@ -79,6 +79,7 @@ const emu_uint3* cur_bid();
 extern emu_uint3 g_grid_dim, g_block_dim;
 void launch(const char* name, dim3 grid, dim3 block, size_t dyn_lds, const std::function<void()>& body);
 void* dyn_lds();
+void* static_lds(int id, size_t bytes);  // per-workgroup __shared__ array (prepare.py)
 emu_f32x4 mfma_16x16x32_bf16(emu_bf16x8 a, emu_bf16x8 b, emu_f32x4 c);
 uint64_t ballot(bool pred);
 uint32_t readfirstlane(uint32_t v);

@@ -16,6 +16,8 @@ CPU.  These tests check, with no GPU:
 * the workspace contract: the decode slot half is zero again after every call
   and the status word stays clear;
 * determinism (two calls, identical bits);
+* LDS: static arrays are per workgroup, poisoned and guarded like the dynamic
+  LDS, and the two together must fit 160 KB (negative control);
 * the GEMM's copy pipeline: direct-to-LDS copies land only at a wait that covers
   them, so a wait one operation short reads stale tiles (negative control);
 * races inside a workgroup: results must not depend on the order in which the
@@ -324,6 +326,42 @@ def test_cross_workgroup_reads_must_be_coherent(tmp_path):
     res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
     assert res.returncode == 97, (res.returncode, res.stdout, res.stderr[-2000:])
     assert "without agent-coherent accesses" in res.stderr and "gemv_kernel" in res.stderr, res.stderr[-2000:]
+
+
+def test_lds_over_160_kb_is_caught(tmp_path):
+    """Negative control for the LDS budget check: static LDS arrays are emulated per
+    workgroup and counted with the dynamic LDS against the 160 KB a gfx950
+    workgroup can hold.  Activation buffers grown by half fit the 4-wave GEMM
+    (97 KB) but not the 8-wave two-K-half GEMM (194 KB), and the emulator stops it."""
+    if clang() is None:
+        pytest.skip("clang++ not available")
+    with open(KERNELS) as f:
+        src = f.read()
+    decl = "__shared__ u32x4_t As0[KW * kATile], As1[KW * kATile];"
+    assert src.count(decl) == 1
+    bad = tmp_path / "w4a16_big_lds.hip"
+    bad.write_text(src.replace(decl, "__shared__ u32x4_t As0[KW * kATile * 3 / 2], As1[KW * kATile * 3 / 2];"))
+    lib_path = build_emulator(str(tmp_path), str(bad))
+    script = textwrap.dedent(f"""
+        import sys
+        import numpy as np
+        sys.path[:0] = [{ROOT!r}, {os.path.join(ROOT, 'tests')!r}]
+        from emu_harness import Emu, problem, reference, run_linear, bf16_value
+        from oracle.tolerance import assert_parity
+        emu = Emu({lib_path!r})
+        m, k, n = 256, 256, 1024      # 4-wave GEMM: fits
+        xb, packed, scale = problem(m, k, n, seed=3)
+        y = run_linear(emu, xb, packed, scale, m, k, n)
+        assert_parity(bf16_value(y).astype(np.float64), reference(xb, packed, scale, m, k, n), "fits")
+        print("4-wave ok", flush=True)
+        m, k, n = 128, 128, 192 * 256  # 192 tiles of 128 x 256: the 8-wave GEMM
+        xb, packed, scale = problem(m, k, n, seed=4)
+        run_linear(emu, xb, packed, scale, m, k, n)
+        print("no fault")
+    """)
+    res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
+    assert res.returncode == 97 and "4-wave ok" in res.stdout, (res.returncode, res.stdout, res.stderr[-2000:])
+    assert "exceeds 160 KB" in res.stderr and "gemm_kernel" in res.stderr, res.stderr[-2000:]
 
 
 SCHEDULE_SHAPES = [(1, 1024, 512), (3, 4096, 1024), (16, 2048, 512), (24, 1024, 640), (40, 512, 320),
