@@ -9,11 +9,10 @@
 //
 // Workgroups are dispatched in order (x fastest, then y; or the reverse) into
 // a number of resident slots (both set by emu_set_concurrency): one by
-// default, so workgroups run one after another, or more for the decode
-// kernels, whose resident workgroups then interleave at every meeting point
-// -- a split-K finisher polls while its publishers still run.
-// (The other kernels keep one slot: their static __shared__ arrays are
-// ordinary host statics, one copy for all workgroups.)
+// default, so workgroups run one after another, or more, so that resident
+// workgroups interleave at every meeting point -- a decode split-K finisher
+// then polls while its publishers still run.  Every workgroup has its own
+// LDS, static arrays included (static_lds).
 //
 // Lanes of one wave that reach different collectives, a state in which no
 // live thread can move, or a kernel that touches memory outside its buffers
@@ -493,7 +492,7 @@ void launch(const char* name, dim3 grid, dim3 block, size_t dyn, const std::func
   g_grid_dim = emu_uint3{grid.x, grid.y, 1};
   g_block_dim = emu_uint3{block.x, 1, 1};
   g_body = &body;
-  const int slots = strstr(name, "gemv_kernel") ? std::max(1, g_concurrency) : 1;
+  const int slots = std::max(1, g_concurrency);
   const uint64_t nblocks = (uint64_t)grid.x * grid.y;
   uint64_t next = 0;
   std::deque<Block*> resident;

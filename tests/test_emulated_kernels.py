@@ -446,6 +446,21 @@ SPLIT_K_SHAPES = [(1, 4096, 512), (1, 12288, 256), (4, 4096, 384), (16, 2048, 51
 
 
 @pytest.mark.parametrize("reverse", [False, True])
+def test_gemm_with_resident_workgroups(emu, reverse):
+    """The GEMM path (row sums, GEMM with and without K split, the split-K reduce)
+    with every workgroup resident and interleaved: the same bits as one at a time."""
+    try:
+        for m, k, n in ((130, 512, 256), (256, 1024, 512), (200, 512, 333)):
+            xb, packed, scale = problem(m, k, n, seed=m + n, quantized=True)
+            set_concurrency(emu, 1)
+            seq = run_linear(emu, xb, packed, scale, m, k, n)
+            set_concurrency(emu, 4096, reverse)
+            assert np.array_equal(seq, run_linear(emu, xb, packed, scale, m, k, n)), (m, k, n, reverse)
+    finally:
+        set_concurrency(emu, 1)
+
+
+@pytest.mark.parametrize("reverse", [False, True])
 def test_split_k_with_resident_workgroups(emu, reverse):
     """Every workgroup of a decode launch resident at once and interleaved at each
     meeting point, dispatched first-to-last or last-to-first: split-K finishers
