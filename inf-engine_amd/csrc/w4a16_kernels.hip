@@ -1878,19 +1878,19 @@ int zero_scratch(void* p, hipStream_t s) {
   return hipStreamSynchronize(s) == hipSuccess ? W4A16_OK : W4A16_ERR_LAUNCH;
 }
 
-// Device address of the current device's scratch, or null (with W4A16_OK)
-// when it has not been set up and `setup` is false.  Set-up is eager work: the
-// address lookup and a zero fill on `s` that completes before the pointer is
-// published, so a set-up scratch is zero for every stream.  Under graph
-// capture that fill would become a node that re-zeroes 96 MiB on every
-// replay, so a stream that is capturing is refused (W4A16_ERR_CAPTURING): one
-// eager call (or w4a16_noalloc_status) on the device sets the scratch up.
-int scratch_for_current_device(hipStream_t s, bool setup, void** out) {
+// Device address of the current device's scratch, set up on the first call
+// on that device.  Set-up is eager work: the address lookup and a zero fill on
+// `s` that completes before the pointer is published, so a set-up scratch is
+// zero for every stream.  Under graph capture that fill would become a node
+// that re-zeroes 96 MiB on every replay, so a stream that is capturing is
+// refused (W4A16_ERR_CAPTURING): one eager call (or w4a16_noalloc_status) on
+// the device sets the scratch up.
+int scratch_for_current_device(hipStream_t s, void** out) {
   *out = nullptr;
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return W4A16_ERR_LAUNCH;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev] && setup) {
+  if (!g_scratch_ptr[dev]) {
     if (capturing(s)) return W4A16_ERR_CAPTURING;
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return W4A16_ERR_LAUNCH;
@@ -1997,7 +1997,7 @@ int w4a16_linear_noalloc(const void* x, int64_t ldx, const int8_t* packed, int64
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (need == 0) return run(&q, 1, nullptr, 0, s);
   void* ws = nullptr;
-  rc = scratch_for_current_device(s, true, &ws);
+  rc = scratch_for_current_device(s, &ws);
   if (rc != W4A16_OK) return rc;
   return run(&q, 1, ws, kScratchBytes, s);
 }
@@ -2018,7 +2018,7 @@ int w4a16_noalloc_status(void* stream, uint32_t* status) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (capturing(s)) return W4A16_ERR_CAPTURING;
   void* ws = nullptr;
-  int rc = scratch_for_current_device(s, true, &ws);
+  int rc = scratch_for_current_device(s, &ws);
   if (rc != W4A16_OK) return rc;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (hipStreamSynchronize(s) != hipSuccess) return W4A16_ERR_LAUNCH;
