@@ -207,11 +207,11 @@ def workspace_size(m: int, n: int, k: int, group_size: int = 128) -> int:
 class _Workspace:
     __slots__ = ("tensor", "captured", "defined", "filled_in")
 
-    def __init__(self, tensor: torch.Tensor, captured: bool, defined: bool, filled_in: set[int]):
+    def __init__(self, tensor: torch.Tensor, captured: bool, defined: bool, filled_in: set[int | None]):
         self.tensor = tensor
         self.captured = captured    # some captured graph holds this buffer's address
         self.defined = defined      # zeroed eagerly: every call leaves its slots empty from then on
-        self.filled_in = filled_in  # ids of the captures that recorded a zero fill of this buffer
+        self.filled_in = filled_in  # ids of the captures that recorded a zero fill (None: unnamed)
 
 
 _workspaces: dict[tuple[int, int], _Workspace] = {}
